@@ -1,0 +1,264 @@
+"""candle-moe for MI355X: Python mirror of the reference's Rust API.
+
+The reference crate exposes (``/root/reference/src/lib.rs``)::
+
+    apply_topk_softmax_inplace(gating_output, topk_weight, topk_indices, token_expert_indices)
+    enum Activation { Silu, Gelu, Relu }
+    FusedMoE::new(num_experts, num_selected_experts, activation)
+    FusedMoE::forward(input, gate, up, down: Option, routing_weights, expert_indices, moe_type)
+
+This module offers the same names, argument meaning and error behaviour over
+torch tensors that live on the GPU (PyTorch is only the device-memory and
+stream plumbing). Every call goes through the C ABI of
+``libcandle_moe_hip.so`` (``include/candle_moe.h``); there is no CPU
+fallback: without the built library every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from typing import Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libcandle_moe_hip.so")
+
+CANDLE_MOE_OK = 0
+CANDLE_MOE_ERR_INVALID = 1
+CANDLE_MOE_ERR_UNSUPPORTED = 2
+CANDLE_MOE_ERR_HIP = 3
+CANDLE_MOE_ERR_WORKSPACE = 4
+
+# descriptor dtype codes (include/candle_moe.h CM_DT_*)
+DT_F16, DT_BF16, DT_F32, DT_U32, DT_I64, DT_F64, DT_U8 = range(7)
+MAX_RANK = 4
+
+
+class CandleMoeError(RuntimeError):
+    """A call was rejected or failed; ``code`` is the CANDLE_MOE_* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class Activation(enum.IntEnum):
+    """Activation codes of the reference (``/root/reference/src/lib.rs:157-172``)."""
+
+    Silu = 0
+    Gelu = 1
+    Relu = 2
+
+    def to_int(self) -> int:
+        return int(self)
+
+
+class CmTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * MAX_RANK),
+        ("strides", ctypes.c_int64 * MAX_RANK),
+        ("device", ctypes.c_int32),
+    ]
+
+
+class CmFusedMoE(ctypes.Structure):
+    _fields_ = [
+        ("num_experts", ctypes.c_int64),
+        ("num_selected_experts", ctypes.c_int64),
+        ("activation", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"candle_moe: {LIB_PATH} is missing; build it with `make -C candle-moe_amd` "
+                "(or __graft_entry__.build()). There is no CPU fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i32, u32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_size_t
+        L.topk_softmax.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp]
+        L.topk_softmax.restype = None
+        L.candle_moe_topk_softmax_status.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp]
+        L.candle_moe_topk_softmax_status.restype = i32
+        L.candle_moe_topk_softmax_ex.argtypes = [vp, i32, vp, i32, vp, vp, i32, i32, i32, vp]
+        L.candle_moe_topk_softmax_ex.restype = i32
+        moe_args = [vp] * 7 + [i32] * 6 + [u32, u32]
+        L.fused_moe.argtypes = moe_args + [vp]
+        L.fused_moe.restype = None
+        L.candle_moe_fused_moe_status.argtypes = moe_args + [vp]
+        L.candle_moe_fused_moe_status.restype = i32
+        L.candle_moe_fused_moe_workspace_size.argtypes = [i32] * 5 + [u32]
+        L.candle_moe_fused_moe_workspace_size.restype = sz
+        L.candle_moe_fused_moe_ws.argtypes = moe_args + [vp, sz, vp]
+        L.candle_moe_fused_moe_ws.restype = i32
+        L.candle_moe_last_error.argtypes = []
+        L.candle_moe_last_error.restype = ctypes.c_char_p
+        L.candle_moe_version.argtypes = []
+        L.candle_moe_version.restype = ctypes.c_char_p
+        tp = ctypes.POINTER(CmTensor)
+        L.candle_moe_apply_topk_softmax_inplace.argtypes = [tp, tp, tp, tp, vp]
+        L.candle_moe_apply_topk_softmax_inplace.restype = i32
+        L.candle_moe_validate_topk_softmax.argtypes = [tp, tp, tp, tp]
+        L.candle_moe_validate_topk_softmax.restype = i32
+        mp = ctypes.POINTER(CmFusedMoE)
+        L.candle_moe_fused_moe_forward.argtypes = [mp, tp, tp, tp, tp, tp, tp, u32, tp, vp]
+        L.candle_moe_fused_moe_forward.restype = i32
+        L.candle_moe_validate_fused_moe.argtypes = [mp, tp, tp, tp, tp, tp, tp, u32, tp]
+        L.candle_moe_validate_fused_moe.restype = i32
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().candle_moe_last_error().decode()
+
+
+def check(code: int) -> None:
+    if code != CANDLE_MOE_OK:
+        raise CandleMoeError(code, last_error())
+
+
+# ------------------------------------------------------------ descriptors
+def _torch_dtype_code(t) -> int:
+    import torch
+
+    m = {
+        torch.float16: DT_F16,
+        torch.bfloat16: DT_BF16,
+        torch.float32: DT_F32,
+        torch.int64: DT_I64,
+        torch.float64: DT_F64,
+        torch.uint8: DT_U8,
+    }
+    if hasattr(torch, "uint32"):
+        m[torch.uint32] = DT_U32
+    # int32 index tensors are taken as u32 bit patterns (torch's uint32
+    # support is partial); values must be non-negative.
+    m[torch.int32] = DT_U32
+    if t.dtype not in m:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, f"dtype {t.dtype} is not supported")
+    return m[t.dtype]
+
+
+def describe(t) -> CmTensor:
+    """cm_tensor_t for a torch tensor (GPU tensors carry their ordinal)."""
+    d = CmTensor()
+    if t.dim() > MAX_RANK:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, f"rank {t.dim()} exceeds {MAX_RANK}")
+    d.data = t.data_ptr() if t.numel() else None
+    d.dtype = _torch_dtype_code(t)
+    d.rank = t.dim()
+    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
+        d.dims[i] = s
+        d.strides[i] = st
+    d.device = t.device.index if t.is_cuda else -1
+    return d
+
+
+def spec(shape: Sequence[int], dtype: int, device: int = 0, strides: Optional[Sequence[int]] = None) -> CmTensor:
+    """A data-less descriptor, for the validation entry points."""
+    d = CmTensor()
+    d.data = None
+    d.dtype = dtype
+    d.rank = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for i, (s, st) in enumerate(zip(shape, strides)):
+        d.dims[i] = s
+        d.strides[i] = st
+    d.device = device
+    return d
+
+
+def _stream_for(t) -> Optional[int]:
+    import torch
+
+    if not t.is_cuda:
+        return None
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# -------------------------------------------------------------- the API
+def apply_topk_softmax_inplace(gating_output, topk_weight, topk_indices, token_expert_indices) -> None:
+    """Router softmax + top-k written in place (``/root/reference/src/lib.rs:124-155``).
+
+    gating_output [T, E]; topk_weight [T, k] of the same dtype (f32, f16 or
+    bf16); topk_indices / token_expert_indices [T, k] u32 (int32 accepted).
+    """
+    g, w, i, ei = (describe(t) for t in (gating_output, topk_weight, topk_indices, token_expert_indices))
+    check(lib().candle_moe_apply_topk_softmax_inplace(
+        ctypes.byref(g), ctypes.byref(w), ctypes.byref(i), ctypes.byref(ei), _stream_for(gating_output)))
+
+
+def validate_topk_softmax(g: CmTensor, w: CmTensor, i: CmTensor, ei: CmTensor) -> None:
+    check(lib().candle_moe_validate_topk_softmax(ctypes.byref(g), ctypes.byref(w), ctypes.byref(i), ctypes.byref(ei)))
+
+
+class FusedMoE:
+    """``FusedMoE`` of the reference (``/root/reference/src/lib.rs:244-335``)."""
+
+    def __init__(self, num_experts: int, num_selected_experts: int, activation: Activation):
+        self.num_experts = int(num_experts)
+        self.num_selected_experts = int(num_selected_experts)
+        self.activation = Activation(activation)
+
+    @classmethod
+    def new(cls, num_experts: int, num_selected_experts: int, activation: Activation) -> "FusedMoE":
+        return cls(num_experts, num_selected_experts, activation)
+
+    def _self(self) -> CmFusedMoE:
+        return CmFusedMoE(self.num_experts, self.num_selected_experts, int(self.activation))
+
+    def forward(self, input, gate_weights, up_weights, down_weights, routing_weights, expert_indices,
+                moe_type: int):
+        """Returns a new [num_tokens, hidden_dim] tensor of input's dtype.
+
+        input [T, H]; gate_weights / up_weights [E, H, I]; down_weights
+        [E, I, H] (Qwen3, moe_type 0) or None (Nomic, moe_type 1);
+        routing_weights [T, k] f32; expert_indices [T, k] u32.
+        """
+        import torch
+
+        out_shape = tuple(input.shape[:1]) + tuple(input.shape[1:2]) if input.dim() == 2 else (0, 0)
+        output = torch.empty(out_shape, dtype=input.dtype, device=input.device)
+        m = self._self()
+        descs = [describe(t) for t in (input, gate_weights, up_weights)]
+        dd = describe(down_weights) if down_weights is not None else None
+        rw, ix, od = describe(routing_weights), describe(expert_indices), describe(output)
+        check(lib().candle_moe_fused_moe_forward(
+            ctypes.byref(m), ctypes.byref(descs[0]), ctypes.byref(descs[1]), ctypes.byref(descs[2]),
+            ctypes.byref(dd) if dd is not None else None, ctypes.byref(rw), ctypes.byref(ix), int(moe_type),
+            ctypes.byref(od), _stream_for(input)))
+        return output
+
+    __call__ = forward
+
+    def validate(self, input: CmTensor, gate: CmTensor, up: CmTensor, down: Optional[CmTensor],
+                 routing: CmTensor, indices: CmTensor, moe_type: int, output: CmTensor) -> None:
+        m = self._self()
+        check(lib().candle_moe_validate_fused_moe(
+            ctypes.byref(m), ctypes.byref(input), ctypes.byref(gate), ctypes.byref(up),
+            ctypes.byref(down) if down is not None else None, ctypes.byref(routing), ctypes.byref(indices),
+            int(moe_type), ctypes.byref(output)))
+
+
+def version() -> str:
+    return lib().candle_moe_version().decode()
+
+
+__all__ = [
+    "Activation", "FusedMoE", "apply_topk_softmax_inplace", "CandleMoeError", "lib", "describe", "spec",
+    "validate_topk_softmax", "version", "LIB_PATH",
+]

@@ -1,0 +1,309 @@
+// C ABI of libcandle_moe_hip.so: the reference's two FFI symbols
+// (/root/reference/src/ffi.rs:15-62), their status-returning variants and
+// the fused-MoE dispatcher (/root/reference/kernels/moe.cu:453-771).
+//
+// Dispatcher, per call, all on the caller's stream, no host sync:
+//   grouping (3 launches) -> GEMM1 (gate+up or fc1, activation fused)
+//   -> zero f32 accumulator -> GEMM2 (down or fc2, routing weight and
+//   scatter-add fused) -> finalize (output += accumulator, rounded once).
+// Workspace (256-byte aligned pieces): offsets[E+2], per-block counts,
+// sorted pair ids, row-tile table, intermediate [T*k, I] in the input dtype
+// and the f32 accumulator [T, H].
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/candle_moe.h"
+#include "cm_common.hpp"
+#include "cm_internal.hpp"
+
+namespace cm {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+static int hip_fail(hipError_t e, const char* what) {
+    return set_error(CANDLE_MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------ router
+int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void* ei, int E, int T, int k,
+                      void* stream) {
+    clear_error();
+    if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: num_tokens must be >= 0 (got %d)", T);
+    if (E < 1 || E > 1024)
+        return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: num_experts must be in [1, 1024] (got %d)", E);
+    if (k < 1 || k > E)
+        return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: topk must be in [1, num_experts=%d] (got %d)", E, k);
+    if (T == 0) return CANDLE_MOE_OK;
+    if (!g || !w || !idx || !ei) return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: null tensor pointer");
+    const hipError_t e = launch_topk_softmax(g, gdt, w, wdt, reinterpret_cast<uint32_t*>(idx),
+                                             reinterpret_cast<uint32_t*>(ei), T, E, k,
+                                             reinterpret_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue && !((gdt == wdt) || wdt == kF32))
+        return set_error(CANDLE_MOE_ERR_UNSUPPORTED, "topk_softmax: unsupported dtype pair (%d, %d)", gdt, wdt);
+    if (e != hipSuccess) return hip_fail(e, "topk_softmax launch");
+    return CANDLE_MOE_OK;
+}
+
+// ------------------------------------------------------------- fused MoE
+struct Problem {
+    int T, H, I, E, k, act, moe_type, dtype;
+    bool mfma;
+    int BM;
+    long long P;
+};
+
+struct Layout {
+    size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles, inter, acc, total;
+};
+
+static size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static Layout make_layout(const Problem& p) {
+    Layout L;
+    const size_t es = p.dtype == kF32 ? 4 : 2;
+    const long long nb = grouping_blocks(p.P);
+    const long long mt = grouping_max_tiles(p.P, p.E, p.BM);
+    size_t o = 0;
+    L.offsets = o; o += a256((size_t)(p.E + 2) * 4);
+    L.block_counts = o; o += a256((size_t)(nb > 0 ? nb : 1) * p.E * 4);
+    L.sorted_pair = o; o += a256((size_t)(p.P > 0 ? p.P : 1) * 4);
+    L.tile_row = o; o += a256((size_t)mt * 4);
+    L.tile_exp = o; o += a256((size_t)mt * 4);
+    L.num_tiles = o; o += 256;
+    L.inter = o; o += a256((size_t)p.P * p.I * es);
+    L.acc = o; o += a256((size_t)p.T * p.H * 4);
+    L.total = o;
+    return L;
+}
+
+static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
+                         Problem& p) {
+    if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
+    if (H < 1 || I < 1)
+        return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: hidden_dim and intermediate_dim must be >= 1 (got %d, %d)", H, I);
+    if (E < 1 || E > 4096)
+        return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_experts must be in [1, 4096] (got %d)", E);
+    if (k < 1) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_selected_experts must be >= 1 (got %d)", k);
+    if (act < 0 || act > 2) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: activation_type must be 0, 1 or 2 (got %d)", act);
+    if (moe_type > 1) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: moe_type must be one of 0 or 1 (got %u)", moe_type);
+    if (dtype > 2) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: dtype must be 0 (f16), 1 (bf16) or 2 (f32) (got %u)", dtype);
+    const long long P = (long long)T * k;
+    if (P > 0x7fffffffLL)
+        return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens * num_selected_experts exceeds 2^31-1");
+    p.T = T; p.H = H; p.I = I; p.E = E; p.k = k; p.act = act; p.moe_type = (int)moe_type; p.dtype = (int)dtype;
+    p.P = P;
+    p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
+    p.BM = p.mfma ? kMfmaBM : kSimtBM;
+    return CANDLE_MOE_OK;
+}
+
+static int run_moe(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
+                   const float* rw, const uint32_t* idx, void* out, char* ws, hipStream_t s) {
+    const Layout L = make_layout(p);
+    GroupingBufs gb;
+    gb.offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    gb.block_counts = reinterpret_cast<int32_t*>(ws + L.block_counts);
+    gb.sorted_pair = reinterpret_cast<int32_t*>(ws + L.sorted_pair);
+    gb.tile_row = reinterpret_cast<int32_t*>(ws + L.tile_row);
+    gb.tile_exp = reinterpret_cast<int32_t*>(ws + L.tile_exp);
+    gb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles);
+    hipError_t e = launch_grouping(idx, p.P, p.E, p.BM, gb, s);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe grouping");
+
+    const bool qwen3 = p.moe_type == kQwen3;
+    const int m_tiles_max = (int)grouping_max_tiles(p.P, p.E, p.BM);
+    void* inter = ws + L.inter;
+    float* acc = reinterpret_cast<float*>(ws + L.acc);
+
+    GemmArgs g1 = {};
+    g1.A = x;
+    g1.B0 = gate;
+    g1.B1 = up;
+    g1.C = inter;
+    g1.routing_w = rw;
+    g1.sorted_pair = gb.sorted_pair;
+    g1.tile_row = gb.tile_row;
+    g1.tile_exp = gb.tile_exp;
+    g1.num_tiles = gb.num_tiles;
+    g1.offsets = gb.offsets;
+    g1.strideB = (long long)p.H * p.I;
+    g1.ldb = p.I;
+    g1.K = p.H;
+    g1.N = p.I;
+    g1.k_top = p.k;
+    g1.act = p.act;
+    const int mode1 = qwen3 ? kGateUp : kFc1;
+    g1.n_tiles = cdiv(p.I, gemm_tile_cols(mode1, p.mfma));
+    g1.m_tiles_max = m_tiles_max;
+    e = launch_moe_gemm(mode1, p.dtype, p.mfma, g1, s);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe gate/up GEMM");
+
+    e = launch_fill_zero_f32(acc, (long long)p.T * p.H, s);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe accumulator clear");
+
+    GemmArgs g2 = g1;
+    g2.A = inter;
+    g2.B0 = qwen3 ? down : up;
+    g2.B1 = nullptr;
+    g2.C = acc;
+    g2.strideB = (long long)p.I * p.H;
+    g2.ldb = qwen3 ? p.H : p.I;
+    g2.K = p.I;
+    g2.N = p.H;
+    const int mode2 = qwen3 ? kDown : kFc2;
+    g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.mfma));
+    e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM");
+
+    e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, s);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe finalize");
+    return CANDLE_MOE_OK;
+}
+
+static int check_ptrs(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
+                      const void* rw, const void* idx, const void* out) {
+    if (p.T == 0) return CANDLE_MOE_OK;
+    if (!x || !gate || !up || !rw || !idx || !out)
+        return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: null tensor pointer");
+    if (p.moe_type == kQwen3 && !down)
+        return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: down_weights is required for moe_type 0 (Qwen3)");
+    return CANDLE_MOE_OK;
+}
+
+// Stream-ordered pool allocation; the pool keeps freed memory (release
+// threshold raised once per device) so repeated calls do not go to the driver.
+static void prepare_pool_once() {
+    static std::mutex mu;
+    static bool done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+    std::lock_guard<std::mutex> lk(mu);
+    if (done[dev]) return;
+    done[dev] = true;
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+        uint64_t thr = ~0ull;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &thr);
+    }
+}
+
+int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
+                   const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, void* stream) {
+    clear_error();
+    Problem p;
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p);
+    if (rc) return rc;
+    rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
+    if (rc) return rc;
+    if (T == 0) return CANDLE_MOE_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const Layout L = make_layout(p);
+    if (!own_ws) {
+        if (!ws || ws_bytes < L.total)
+            return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: workspace of %zu bytes is smaller than the %zu required",
+                             ws_bytes, L.total);
+        if ((uintptr_t)ws % 256)
+            return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: workspace must be 256-byte aligned");
+        return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw),
+                       reinterpret_cast<const uint32_t*>(idx), out, reinterpret_cast<char*>(ws), s);
+    }
+    prepare_pool_once();
+    void* mem = nullptr;
+    hipError_t e = hipMallocAsync(&mem, L.total, s);
+    if (e != hipSuccess) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s",
+                                          L.total, hipGetErrorString(e));
+    rc = run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
+                 out, reinterpret_cast<char*>(mem), s);
+    e = hipFreeAsync(mem, s);
+    if (rc == CANDLE_MOE_OK && e != hipSuccess) return hip_fail(e, "fused_moe: hipFreeAsync");
+    return rc;
+}
+
+size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
+    Problem p;
+    if (check_problem(T, H, I, E, k, 0, 0, dtype, p)) return 0;
+    return make_layout(p).total;
+}
+
+}  // namespace cm
+
+// ----------------------------------------------------------------- C ABI
+extern "C" {
+
+void topk_softmax(const void* gating_output, void* topk_weight, void* topk_indices, void* token_expert_indices,
+                  int num_experts, int num_tokens, int topk, void* stream) {
+    (void)cm::topk_softmax_impl(gating_output, cm::kF32, topk_weight, cm::kF32, topk_indices, token_expert_indices,
+                                num_experts, num_tokens, topk, stream);
+}
+
+int candle_moe_topk_softmax_status(const void* gating_output, void* topk_weight, void* topk_indices,
+                                   void* token_expert_indices, int num_experts, int num_tokens, int topk,
+                                   void* stream) {
+    return cm::topk_softmax_impl(gating_output, cm::kF32, topk_weight, cm::kF32, topk_indices, token_expert_indices,
+                                 num_experts, num_tokens, topk, stream);
+}
+
+int candle_moe_topk_softmax_ex(const void* gating_output, int gating_dtype, void* topk_weight, int weight_dtype,
+                               void* topk_indices, void* token_expert_indices, int num_experts, int num_tokens,
+                               int topk, void* stream) {
+    if (gating_dtype < 0 || gating_dtype > 2 || weight_dtype < 0 || weight_dtype > 2)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: dtype codes must be 0, 1 or 2");
+    return cm::topk_softmax_impl(gating_output, gating_dtype, topk_weight, weight_dtype, topk_indices,
+                                 token_expert_indices, num_experts, num_tokens, topk, stream);
+}
+
+void fused_moe(const void* input, const void* gate_weights, const void* up_weights, const void* down_weights,
+               const void* routing_weights, const void* expert_indices, void* output, int num_tokens, int hidden_dim,
+               int intermediate_dim, int num_experts, int num_selected_experts, int activation_type,
+               uint32_t moe_type, uint32_t dtype, void* stream) {
+    (void)cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
+                             num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
+                             activation_type, moe_type, dtype, nullptr, 0, true, stream);
+}
+
+int candle_moe_fused_moe_status(const void* input, const void* gate_weights, const void* up_weights,
+                                const void* down_weights, const void* routing_weights, const void* expert_indices,
+                                void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+                                void* stream) {
+    return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
+                              num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
+                              activation_type, moe_type, dtype, nullptr, 0, true, stream);
+}
+
+size_t candle_moe_fused_moe_workspace_size(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                           int num_selected_experts, uint32_t dtype) {
+    return cm::fused_moe_ws_size(num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts, dtype);
+}
+
+int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const void* up_weights,
+                            const void* down_weights, const void* routing_weights, const void* expert_indices,
+                            void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                            int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+    return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
+                              num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
+                              activation_type, moe_type, dtype, workspace, workspace_bytes, false, stream);
+}
+
+const char* candle_moe_last_error(void) { return cm::g_last_error.c_str(); }
+
+const char* candle_moe_version(void) { return "candle-moe-hip 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// Internal launcher interface between the kernels and the C-ABI dispatcher.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cm {
+
+// ---------------------------------------------------------------- router
+hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_dtype, uint32_t* idx,
+                               uint32_t* ei, int T, int E, int k, hipStream_t stream);
+
+// -------------------------------------------------------------- grouping
+// Pairs p = t*k + j are grouped by expert idx[p] (stable: ascending p inside
+// an expert). Pairs whose expert is >= E are dropped, as in
+// /root/reference/kernels/preprocessing.cuh:49-52.
+struct GroupingBufs {
+    int32_t* offsets;       // [E+2]: exclusive scan, [E] = valid pairs, [E+1] = max count
+    int32_t* block_counts;  // [nblocks * E]
+    int32_t* sorted_pair;   // [P]
+    int32_t* tile_row;      // [max_tiles]: first sorted row of the tile
+    int32_t* tile_exp;      // [max_tiles]: expert of the tile
+    int32_t* num_tiles;     // [1]
+};
+constexpr int kGroupChunk = 4096;  // pairs per grouping workgroup
+inline int grouping_blocks(long long P) { return (int)((P + kGroupChunk - 1) / kGroupChunk); }
+inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM - 1) / BM + E; }
+hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
+                           hipStream_t stream);
+
+// ----------------------------------------------------------- grouped GEMM
+enum GemmMode : int {
+    kGateUp = 0,  // Qwen3: inter = act(x.G) * (x.U)      (A gathered from x, B [K,N] x2)
+    kFc1 = 1,     // Nomic: inter = act(x.G)              (A gathered from x, B [K,N])
+    kDown = 2,    // Qwen3: acc[t] += w * (inter.D)       (A = inter rows, B [K,N])
+    kFc2 = 3,     // Nomic: acc[t] += w * (inter.U^T)     (A = inter rows, B [N,K])
+};
+
+struct GemmArgs {
+    const void* A;            // x [T,K] (kGateUp/kFc1) or inter [P,K] (kDown/kFc2)
+    const void* B0;           // gate / down / up weights, expert-major
+    const void* B1;           // up weights (kGateUp)
+    void* C;                  // inter [P,N] (dtype) or f32 accumulator [T,N]
+    const float* routing_w;   // [T*k]
+    const int32_t* sorted_pair;
+    const int32_t* tile_row;
+    const int32_t* tile_exp;
+    const int32_t* num_tiles;
+    const int32_t* offsets;
+    long long strideB;        // elements between consecutive experts' B matrices
+    int ldb;                  // row pitch of B in elements
+    int K;                    // reduction length
+    int N;                    // logical output columns
+    int k_top;                // pair -> token divisor
+    int act;                  // activation code
+    int n_tiles;              // output column tiles
+    int m_tiles_max;          // upper bound on row tiles (grid sizing)
+};
+
+// Row tile used by the grouping tile table for the MFMA GEMMs.
+constexpr int kMfmaBM = 128;
+constexpr int kSimtBM = 64;
+
+bool mfma_supported(int dtype, int K, int N);
+// Logical output columns covered by one workgroup of the chosen kernel.
+int gemm_tile_cols(int mode, bool use_mfma);
+hipError_t launch_moe_gemm(int mode, int dtype, bool use_mfma, const GemmArgs& a, hipStream_t stream);
+
+// f32 accumulator helpers
+hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);
+hipError_t launch_fill_zero_bytes(void* p, long long nbytes, hipStream_t stream);
+// out[i] = dtype(out[i] + acc[i])
+hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, hipStream_t stream);
+
+// ------------------------------------------------------------ C-ABI core
+// Record the message of a failing call (thread-local) and return `code`.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void* ei, int E, int T, int k,
+                      void* stream);
+int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
+                   const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, void* stream);
+
+}  // namespace cm

@@ -1,0 +1,486 @@
+// Expert-grouped GEMMs of the fused MoE layer.
+//
+// Four products, one per GemmMode (/root/reference/kernels/moe.cu:193-449 for
+// the f32 reference kernels, /root/reference/kernels/qwen3_moe.cu and
+// nomic_moe.cu for the 16-bit ones):
+//   kGateUp  Qwen3 gate+up : inter[r] = act(x_t . G_e) * (x_t . U_e)
+//   kFc1     Nomic fc1     : inter[r] = act(x_t . G_e)
+//   kDown    Qwen3 down    : acc[t]  += w_p * (inter[r] . D_e)
+//   kFc2     Nomic fc2     : acc[t]  += w_p * (inter[r] . U_e^T)
+// where r runs over expert-sorted pairs p = t*k + j of expert e and acc is
+// an f32 [T,N] accumulator that a final pass adds to the caller's output.
+//
+// moe_mfma_gemm (bf16 / f16): 256 threads = 4 waves in a 2x2 layout, block
+// tile BM x BN, K staged 64 at a time through a 2-stage LDS ring.
+//  * A rows are gathered per tile row (token of the pair) with 16-byte loads.
+//  * Weights stored [K,N] (N contiguous) are loaded as 8x8 blocks and
+//    transposed in registers with v_perm_b32 so LDS holds every operand
+//    K-contiguous; [N,K] weights (Nomic fc2) are copied as they are.
+//  * LDS rows are 128 B with an XOR swizzle of the 16-byte chunk index by
+//    row bits [2:0] and [5:3], so fragment reads and transposed writes hit
+//    distinct banks.
+//  * v_mfma_f32_32x32x16_{bf16,f16} with the weight fragment as the MFMA A
+//    operand: each lane then owns 4 consecutive output columns of one row,
+//    which the epilogue writes as one 8-byte store (or 4 f32 atomics).
+//  * gate and up column blocks are interleaved every 32 columns, so the
+//    SwiGLU product is formed in registers.
+//  * Workgroup ids are remapped so each XCD walks a contiguous range of
+//    tiles, column tiles of one row tile adjacent (A reuse in that XCD's L2).
+// moe_simt_gemm: f32 (and any shape the MFMA path does not take), 64x64
+// tiles with 4x4 outputs per thread.
+#include "cm_common.hpp"
+#include "cm_internal.hpp"
+
+namespace cm {
+
+constexpr int kBK = 64;  // K elements per LDS stage
+
+__device__ __forceinline__ int swz(int row, int c) { return row * 128 + (((c ^ row ^ (row >> 3)) & 7) << 4); }
+
+// Bijective remap of the hardware dispatch order (workgroup w runs on XCD
+// w % 8) to a logical tile id that is contiguous per XCD.
+__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
+    const int nwg = gridDim.x;
+    const int w = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
+    const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
+    mt = logical / n_tiles;
+    nt = logical - mt * n_tiles;
+}
+
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+template <int DT, int BM, int BN, int MODE>
+__global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
+    constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 32, NB = WN / 32;
+    constexpr bool DUAL = (MODE == kGateUp);
+    constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
+    constexpr bool BNK = (MODE == kFc2);
+    constexpr int A_ITEMS = BM * 8 / 256;
+    constexpr int B_ITEMS = BNK ? (BN * 8 / 256) : ((BN + 255) / 256);  // 16-B chunks or 8x8 blocks
+    constexpr int B_REGS = BNK ? B_ITEMS : B_ITEMS * 8;
+    constexpr int STAGE = (BM + BN) * 128;
+    static_assert(!DUAL || (WN % 64) == 0, "gate/up pairs must stay inside one wave");
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    int mt, nt;
+    tile_coords(a.n_tiles, mt, nt);
+    if (mt >= *a.num_tiles) return;
+    const int r0 = a.tile_row[mt];
+    const int e = a.tile_exp[mt];
+    const int seg_end = a.offsets[e + 1];
+    const int m_valid = min(BM, seg_end - r0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int K = a.K, N = a.N;
+
+    const uint16_t* Ab = reinterpret_cast<const uint16_t*>(a.A);
+    const uint16_t* B0 = reinterpret_cast<const uint16_t*>(a.B0) + (long long)e * a.strideB;
+    const uint16_t* B1 = DUAL ? reinterpret_cast<const uint16_t*>(a.B1) + (long long)e * a.strideB : nullptr;
+
+    // A: thread owns chunk (tid & 7) of rows (tid >> 3) + 32 i.
+    const int a_c = tid & 7;
+    long long a_off[A_ITEMS];
+#pragma unroll
+    for (int i = 0; i < A_ITEMS; ++i) {
+        const int r = (tid >> 3) + 32 * i;
+        const int rr = r < m_valid ? r : 0;
+        if constexpr (GATHER) {
+            const int tok = a.sorted_pair[r0 + rr] / a.k_top;
+            a_off[i] = (long long)tok * K;
+        } else {
+            a_off[i] = (long long)(r0 + rr) * K;
+        }
+    }
+    // B source pointers and validity.
+    const uint16_t* b_ptr[B_ITEMS];
+    bool b_ok[B_ITEMS];
+    int b_kb[B_ITEMS], b_q[B_ITEMS];
+#pragma unroll
+    for (int i = 0; i < B_ITEMS; ++i) {
+        const int item = tid + 256 * i;
+        if constexpr (BNK) {
+            const int row = item >> 3, c = item & 7;
+            const int col = nt * BN + row;
+            b_ok[i] = col < N;
+            b_ptr[i] = B0 + (long long)(b_ok[i] ? col : 0) * a.ldb + c * 8;
+            b_kb[i] = c;
+            b_q[i] = row;
+        } else {
+            const int q = item % (BN / 8), kb = item / (BN / 8);
+            const int nr = q * 8;
+            int col;
+            const uint16_t* base;
+            if constexpr (DUAL) {
+                col = nt * (BN / 2) + (nr >> 6) * 32 + (nr & 31);
+                base = ((nr >> 5) & 1) ? B1 : B0;
+            } else {
+                col = nt * BN + nr;
+                base = B0;
+            }
+            b_ok[i] = (item < BN) && (col < N);
+            b_ptr[i] = base + (long long)kb * 8 * a.ldb + (b_ok[i] ? col : 0);
+            b_kb[i] = kb;
+            b_q[i] = q;
+        }
+    }
+
+    f32x16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    u32x4 ra[A_ITEMS];
+    u32x4 rb[B_REGS];
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+    auto load_tiles = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < A_ITEMS; ++i) {
+            const bool ok = (k0 + a_c * 8) < K;
+            ra[i] = ok ? *reinterpret_cast<const u32x4*>(Ab + a_off[i] + k0 + a_c * 8) : zero4;
+        }
+#pragma unroll
+        for (int i = 0; i < B_ITEMS; ++i) {
+            if constexpr (BNK) {
+                const bool ok = b_ok[i] && (k0 + b_kb[i] * 8) < K;
+                rb[i] = ok ? *reinterpret_cast<const u32x4*>(b_ptr[i] + k0) : zero4;
+            } else {
+                const bool ok = b_ok[i] && (k0 + b_kb[i] * 8) < K;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    rb[i * 8 + j] = ok ? *reinterpret_cast<const u32x4*>(b_ptr[i] + (long long)(k0 + j) * a.ldb) : zero4;
+            }
+        }
+    };
+    auto store_tiles = [&](int stage) {
+        char* sA = smem + stage * STAGE;
+        char* sB = sA + BM * 128;
+#pragma unroll
+        for (int i = 0; i < A_ITEMS; ++i) {
+            const int r = (tid >> 3) + 32 * i;
+            *reinterpret_cast<u32x4*>(sA + swz(r, a_c)) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_ITEMS; ++i) {
+            if constexpr (BNK) {
+                *reinterpret_cast<u32x4*>(sB + swz(b_q[i], b_kb[i])) = rb[i];
+            } else {
+                if (tid + 256 * i < BN) {
+                    // rb[i*8 + j] holds row k = kb*8 + j, columns q*8 .. q*8+7.
+                    // Transposed: n-row q*8 + c gets k-values kb*8 .. kb*8+7.
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        u32x4 o;
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const uint32_t lo = rb[i * 8 + 2 * d][c >> 1];
+                            const uint32_t hi = rb[i * 8 + 2 * d + 1][c >> 1];
+                            o[d] = (c & 1) ? pack_hi(lo, hi) : pack_lo(lo, hi);
+                        }
+                        *reinterpret_cast<u32x4*>(sB + swz(b_q[i] * 8 + c, b_kb[i])) = o;
+                    }
+                }
+            }
+        }
+    };
+    auto compute = [&](int stage) {
+        const char* sA = smem + stage * STAGE;
+        const char* sB = sA + BM * 128;
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int c = kk * 2 + (lane >> 5);
+            u32x4 af[MB], bf[NB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                af[mb] = *reinterpret_cast<const u32x4*>(sA + swz(wm * WM + mb * 32 + (lane & 31), c));
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                bf[nb] = *reinterpret_cast<const u32x4*>(sB + swz(wn * WN + nb * 32 + (lane & 31), c));
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<DT>(bf[nb], af[mb], acc[mb][nb]);
+        }
+    };
+
+    const int nk = (K + kBK - 1) / kBK;
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) load_tiles((kt + 1) * kBK);
+        compute(cur);
+        if (kt + 1 < nk) store_tiles(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---------------- epilogue: lane owns row (lane & 31), 4 consecutive columns
+    const int nsub = 4 * (lane >> 5);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int ml = wm * WM + mb * 32 + (lane & 31);
+        if (ml >= m_valid) continue;
+        const int r = r0 + ml;
+        if constexpr (MODE == kGateUp || MODE == kFc1) {
+            uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)r * N;
+            constexpr int PAIRS = DUAL ? NB / 2 : NB;
+#pragma unroll
+            for (int q = 0; q < PAIRS; ++q) {
+                const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = colbase + 8 * g + nsub;
+                    if (col >= N) continue;
+                    float h[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if constexpr (DUAL) {
+                            h[j] = act_f32(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
+                        } else {
+                            h[j] = act_f32(acc[mb][q][4 * g + j], a.act);
+                        }
+                    }
+                    u32x2 v;
+                    v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
+                    v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                    *reinterpret_cast<u32x2*>(C + col) = v;
+                }
+            }
+        } else {
+            const int p = a.sorted_pair[r];
+            const int tok = p / a.k_top;
+            const float w = a.routing_w[p];
+            float* C = reinterpret_cast<float*>(a.C) + (long long)tok * N;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int colbase = nt * BN + wn * WN + nb * 32;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = colbase + 8 * g + nsub;
+                    if (col >= N) continue;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) unsafeAtomicAdd(C + col + j, w * acc[mb][nb][4 * g + j]);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ SIMT
+template <int DT, int MODE>
+__global__ __launch_bounds__(256) void moe_simt_gemm(GemmArgs a) {
+    constexpr int TM = 64, TN = 64, TK = 16;
+    constexpr bool DUAL = (MODE == kGateUp);
+    constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
+    constexpr bool BNK = (MODE == kFc2);
+    typedef typename Elem<DT>::storage S;
+    __shared__ float sA[TK][TM + 4];
+    __shared__ float sB[DUAL ? 2 : 1][TK][TN + 4];
+    __shared__ long long s_row[TM];
+
+    int mt, nt;
+    tile_coords(a.n_tiles, mt, nt);
+    if (mt >= *a.num_tiles) return;
+    const int r0 = a.tile_row[mt];
+    const int e = a.tile_exp[mt];
+    const int m_valid = min(TM, a.offsets[e + 1] - r0);
+    const int K = a.K, N = a.N;
+    const int tid = threadIdx.x;
+    const int ty = tid >> 4, tx = tid & 15;
+    const S* A = reinterpret_cast<const S*>(a.A);
+    const S* B0 = reinterpret_cast<const S*>(a.B0) + (long long)e * a.strideB;
+    const S* B1 = DUAL ? reinterpret_cast<const S*>(a.B1) + (long long)e * a.strideB : nullptr;
+    if (tid < TM) {
+        const int rr = tid < m_valid ? tid : 0;
+        if constexpr (GATHER) s_row[tid] = (long long)(a.sorted_pair[r0 + rr] / a.k_top) * K;
+        else s_row[tid] = (long long)(r0 + rr) * K;
+    }
+    __syncthreads();
+    const int n0 = nt * TN;
+    float acc[DUAL ? 2 : 1][4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += TK) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int li = tid + 256 * i;  // 0..1023
+            const int m = li >> 4, kk = li & 15;
+            sA[kk][m] = (k0 + kk < K) ? Elem<DT>::to_f32(A[s_row[m] + k0 + kk]) : 0.0f;
+            const int bk = li >> 6, bn = li & 63;
+#pragma unroll
+            for (int d = 0; d < (DUAL ? 2 : 1); ++d) {
+                const S* B = d ? B1 : B0;
+                float v = 0.0f;
+                if (k0 + bk < K && n0 + bn < N) {
+                    if constexpr (BNK) v = Elem<DT>::to_f32(B[(long long)(n0 + bn) * a.ldb + k0 + bk]);
+                    else v = Elem<DT>::to_f32(B[(long long)(k0 + bk) * a.ldb + n0 + bn]);
+                }
+                sB[d][bk][bn] = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < TK; ++kk) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
+#pragma unroll
+            for (int d = 0; d < (DUAL ? 2 : 1); ++d) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bv[j] = sB[d][kk][tx * 4 + j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[d][i][j] = fmaf(av[i], bv[j], acc[d][i][j]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ml = ty * 4 + i;
+        if (ml >= m_valid) continue;
+        const int r = r0 + ml;
+        if constexpr (MODE == kGateUp || MODE == kFc1) {
+            S* C = reinterpret_cast<S*>(a.C) + (long long)r * N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + tx * 4 + j;
+                if (col >= N) continue;
+                float h = act_f32(acc[0][i][j], a.act);
+                if constexpr (DUAL) h *= acc[DUAL ? 1 : 0][i][j];
+                C[col] = Elem<DT>::from_f32(h);
+            }
+        } else {
+            const int p = a.sorted_pair[r];
+            const float w = a.routing_w[p];
+            float* C = reinterpret_cast<float*>(a.C) + (long long)(p / a.k_top) * N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + tx * 4 + j;
+                if (col < N) unsafeAtomicAdd(C + col, w * acc[0][i][j]);
+            }
+        }
+    }
+}
+
+// -------------------------------------------------------------- helpers
+__global__ void fill_zero_u32(uint32_t* __restrict__ p, long long n) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
+__global__ void fill_zero_u32x4(u32x4* __restrict__ p, long long n) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = z;
+}
+
+template <int DT>
+__global__ void finalize_kernel(typename Elem<DT>::storage* __restrict__ out, const float* __restrict__ acc,
+                                long long n) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = Elem<DT>::from_f32(Elem<DT>::to_f32(out[i]) + acc[i]);
+}
+
+static unsigned grid_for(long long n, int block) {
+    long long g = (n + block - 1) / block;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (unsigned)g;
+}
+
+__global__ void fill_zero_u16(uint16_t* __restrict__ p, long long n) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
+// Zero nbytes (a multiple of 2) with a fill kernel rather than hipMemsetAsync.
+hipError_t launch_fill_zero_bytes(void* p, long long nbytes, hipStream_t stream) {
+    if (nbytes <= 0) return hipSuccess;
+    if (((uintptr_t)p % 16) == 0 && nbytes % 16 == 0) {
+        const long long n = nbytes / 16;
+        hipLaunchKernelGGL(fill_zero_u32x4, dim3(grid_for(n, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<u32x4*>(p), n);
+    } else if (((uintptr_t)p % 4) == 0 && nbytes % 4 == 0) {
+        const long long n = nbytes / 4;
+        hipLaunchKernelGGL(fill_zero_u32, dim3(grid_for(n, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<uint32_t*>(p), n);
+    } else {
+        const long long n = nbytes / 2;
+        hipLaunchKernelGGL(fill_zero_u16, dim3(grid_for(n, 256)), dim3(256), 0, stream,
+                           reinterpret_cast<uint16_t*>(p), n);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream) {
+    return launch_fill_zero_bytes(p, n * 4, stream);
+}
+
+hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 g(grid_for(n, 256)), b(256);
+    if (dtype == kBF16)
+        hipLaunchKernelGGL(finalize_kernel<kBF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n);
+    else if (dtype == kF16)
+        hipLaunchKernelGGL(finalize_kernel<kF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n);
+    else
+        hipLaunchKernelGGL(finalize_kernel<kF32>, g, b, 0, stream, reinterpret_cast<float*>(out), acc, n);
+    return hipGetLastError();
+}
+
+bool mfma_supported(int dtype, int K, int N) {
+    return (dtype == kBF16 || dtype == kF16) && (K % 8 == 0) && (N % 8 == 0);
+}
+
+constexpr int kMfmaBN = 128;
+
+int gemm_tile_cols(int mode, bool use_mfma) {
+    if (!use_mfma) return 64;
+    return mode == kGateUp ? kMfmaBN / 2 : kMfmaBN;
+}
+
+template <int DT, int MODE>
+static hipError_t launch_mode(bool use_mfma, const GemmArgs& a, hipStream_t stream) {
+    if (use_mfma) {
+        if constexpr (DT == kF32) {
+            return hipErrorInvalidValue;
+        } else {
+            constexpr int BM = kMfmaBM, BN = kMfmaBN;
+            const int nwg = a.m_tiles_max * a.n_tiles;
+            if (nwg <= 0) return hipSuccess;
+            hipLaunchKernelGGL((moe_mfma_gemm<DT, BM, BN, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+        }
+    } else {
+        const int nwg = a.m_tiles_max * a.n_tiles;
+        if (nwg <= 0) return hipSuccess;
+        hipLaunchKernelGGL((moe_simt_gemm<DT, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_dt(int mode, bool use_mfma, const GemmArgs& a, hipStream_t stream) {
+    switch (mode) {
+        case kGateUp: return launch_mode<DT, kGateUp>(use_mfma, a, stream);
+        case kFc1: return launch_mode<DT, kFc1>(use_mfma, a, stream);
+        case kDown: return launch_mode<DT, kDown>(use_mfma, a, stream);
+        case kFc2: return launch_mode<DT, kFc2>(use_mfma, a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_moe_gemm(int mode, int dtype, bool use_mfma, const GemmArgs& a, hipStream_t stream) {
+    if (dtype == kBF16) return launch_dt<kBF16>(mode, use_mfma, a, stream);
+    if (dtype == kF16) return launch_dt<kF16>(mode, use_mfma, a, stream);
+    if (dtype == kF32) return launch_dt<kF32>(mode, use_mfma, a, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace cm

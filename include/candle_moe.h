@@ -1,0 +1,177 @@
+/*
+ * candle-moe for MI355X (gfx950): C ABI of libcandle_moe_hip.so.
+ *
+ * The first two symbols are the drop-in boundary: the same names, argument
+ * order, meaning and codes as the reference's FFI, so a Rust (or any C)
+ * caller that binds them needs no change other than linking this library.
+ * Everything is stream-ordered and asynchronous on `stream` (NULL = the
+ * default stream); all tensors are caller-owned, row-major, contiguous
+ * device memory.
+ *
+ * Codes:  activation 0 = SiLU, 1 = GELU (tanh approximation), 2 = ReLU
+ *         moe_type   0 = Qwen3 (gate, up -> down), 1 = Nomic (fc1 -> fc2)
+ *         dtype      0 = f16, 1 = bf16, 2 = f32
+ * Routing weights are always f32, expert indices always u32.
+ */
+#ifndef CANDLE_MOE_H
+#define CANDLE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes of the *_status / host-API entry points. */
+enum {
+    CANDLE_MOE_OK = 0,
+    CANDLE_MOE_ERR_INVALID = 1,     /* argument / shape / dtype rejected before any launch */
+    CANDLE_MOE_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+    CANDLE_MOE_ERR_HIP = 3,         /* a HIP runtime call or launch failed */
+    CANDLE_MOE_ERR_WORKSPACE = 4    /* caller workspace too small / allocation failed */
+};
+
+/* ---------------------------------------------------------------------
+ * Drop-in symbols
+ * ------------------------------------------------------------------- */
+
+/*
+ * Router: softmax over num_experts logits per token, then the top-k.
+ * Replaces the reference symbol declared at /root/reference/src/ffi.rs:15-24
+ * (defined at /root/reference/kernels/topk_softmax.cu:331-353).
+ *   gating_output        [num_tokens, num_experts] f32
+ *   topk_weight          [num_tokens, topk] f32   (descending probability)
+ *   topk_indices         [num_tokens, topk] u32   (ties -> lower expert index)
+ *   token_expert_indices [num_tokens, topk] u32   (= j * num_tokens + t)
+ * num_tokens is a C int, as the reference caller passes it (the reference
+ * definition's int64_t parameter did not match its caller). On invalid
+ * sizes nothing is launched and candle_moe_last_error() says why.
+ */
+void topk_softmax(const void* gating_output, void* topk_weight, void* topk_indices,
+                  void* token_expert_indices, int num_experts, int num_tokens, int topk,
+                  void* stream);
+
+/*
+ * Fused MoE forward: output[t] += sum_j w[t,j] * expert_{idx[t,j]}(input[t]).
+ * Replaces the reference symbol declared at /root/reference/src/ffi.rs:45-62
+ * (defined at /root/reference/kernels/moe.cu:453-771).
+ *   input          [num_tokens, hidden_dim]                       dtype
+ *   gate_weights   [num_experts, hidden_dim, intermediate_dim]    dtype
+ *   up_weights     [num_experts, hidden_dim, intermediate_dim]    dtype
+ *   down_weights   [num_experts, intermediate_dim, hidden_dim]    dtype (Qwen3; NULL for Nomic)
+ *   routing_weights[num_tokens, num_selected_experts]             f32
+ *   expert_indices [num_tokens, num_selected_experts]             u32
+ *   output         [num_tokens, hidden_dim]                       dtype, zero-initialised by
+ *                                                                 the caller (results are added)
+ * Qwen3: y = (act(x G) * (x U)) D.   Nomic: y = act(x G) U^T.
+ * The workspace is taken from the device's stream-ordered memory pool
+ * (hipMallocAsync / hipFreeAsync on `stream`); no host synchronisation.
+ */
+void fused_moe(const void* input, const void* gate_weights, const void* up_weights,
+               const void* down_weights, const void* routing_weights, const void* expert_indices,
+               void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+               int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+               void* stream);
+
+/* ---------------------------------------------------------------------
+ * Status-returning variants of the two symbols (the reference returns
+ * nothing and checks nothing). Same arguments; return a CANDLE_MOE_* code.
+ * ------------------------------------------------------------------- */
+int candle_moe_topk_softmax_status(const void* gating_output, void* topk_weight, void* topk_indices,
+                                   void* token_expert_indices, int num_experts, int num_tokens,
+                                   int topk, void* stream);
+
+/* Router with 16-bit logits / weights (dtype codes above for each tensor).
+ * The reference accepts f16/bf16 topk_weight at /root/reference/src/lib.rs:130-148
+ * but its kernel reads them as f32; this entry point implements them. */
+int candle_moe_topk_softmax_ex(const void* gating_output, int gating_dtype, void* topk_weight,
+                               int weight_dtype, void* topk_indices, void* token_expert_indices,
+                               int num_experts, int num_tokens, int topk, void* stream);
+
+int candle_moe_fused_moe_status(const void* input, const void* gate_weights, const void* up_weights,
+                                const void* down_weights, const void* routing_weights,
+                                const void* expert_indices, void* output, int num_tokens,
+                                int hidden_dim, int intermediate_dim, int num_experts,
+                                int num_selected_experts, int activation_type, uint32_t moe_type,
+                                uint32_t dtype, void* stream);
+
+/* Caller-provided workspace: bytes needed by candle_moe_fused_moe_ws for
+ * these sizes (0 when the arguments are invalid). */
+size_t candle_moe_fused_moe_workspace_size(int num_tokens, int hidden_dim, int intermediate_dim,
+                                           int num_experts, int num_selected_experts,
+                                           uint32_t dtype);
+
+/* fused_moe with a caller-owned device workspace of >= workspace_size bytes
+ * (256-byte aligned); allocates nothing. */
+int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const void* up_weights,
+                            const void* down_weights, const void* routing_weights,
+                            const void* expert_indices, void* output, int num_tokens,
+                            int hidden_dim, int intermediate_dim, int num_experts,
+                            int num_selected_experts, int activation_type, uint32_t moe_type,
+                            uint32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* candle_moe_last_error(void);
+const char* candle_moe_version(void);
+
+/* ---------------------------------------------------------------------
+ * Host API: the reference's Rust surface (/root/reference/src/lib.rs) over
+ * tensor descriptors, with the same validation and error text.
+ * ------------------------------------------------------------------- */
+enum {
+    CM_DT_F16 = 0,
+    CM_DT_BF16 = 1,
+    CM_DT_F32 = 2,
+    CM_DT_U32 = 3,
+    CM_DT_I64 = 4,
+    CM_DT_F64 = 5,
+    CM_DT_U8 = 6
+};
+
+#define CM_MAX_RANK 4
+typedef struct {
+    void* data;                 /* address of element 0 (start offset applied) */
+    int32_t dtype;              /* CM_DT_* */
+    int32_t rank;
+    int64_t dims[CM_MAX_RANK];
+    int64_t strides[CM_MAX_RANK]; /* in elements */
+    int32_t device;             /* GPU ordinal, or -1 for host memory */
+} cm_tensor_t;
+
+typedef struct {
+    int64_t num_experts;
+    int64_t num_selected_experts;
+    int32_t activation;         /* 0 SiLU, 1 GELU, 2 ReLU */
+} cm_fused_moe_t;
+
+/* apply_topk_softmax_inplace (/root/reference/src/lib.rs:124-155). */
+int candle_moe_apply_topk_softmax_inplace(const cm_tensor_t* gating_output, const cm_tensor_t* topk_weight,
+                                          const cm_tensor_t* topk_indices,
+                                          const cm_tensor_t* token_expert_indices, void* stream);
+
+/* FusedMoE::forward (/root/reference/src/lib.rs:273-335). `output` is the
+ * [num_tokens, hidden_dim] tensor of the input dtype that forward returns in
+ * the reference; it is zeroed here (Tensor::zeros at lib.rs:296) before the
+ * launch. down_weights may be NULL (Rust None). */
+int candle_moe_fused_moe_forward(const cm_fused_moe_t* moe, const cm_tensor_t* input,
+                                 const cm_tensor_t* gate_weights, const cm_tensor_t* up_weights,
+                                 const cm_tensor_t* down_weights, const cm_tensor_t* routing_weights,
+                                 const cm_tensor_t* expert_indices, uint32_t moe_type,
+                                 const cm_tensor_t* output, void* stream);
+
+/* The validation half of the two calls above, without launching anything
+ * (runs without a GPU). Returns CANDLE_MOE_OK or CANDLE_MOE_ERR_INVALID. */
+int candle_moe_validate_topk_softmax(const cm_tensor_t* gating_output, const cm_tensor_t* topk_weight,
+                                     const cm_tensor_t* topk_indices,
+                                     const cm_tensor_t* token_expert_indices);
+int candle_moe_validate_fused_moe(const cm_fused_moe_t* moe, const cm_tensor_t* input,
+                                  const cm_tensor_t* gate_weights, const cm_tensor_t* up_weights,
+                                  const cm_tensor_t* down_weights, const cm_tensor_t* routing_weights,
+                                  const cm_tensor_t* expert_indices, uint32_t moe_type,
+                                  const cm_tensor_t* output);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CANDLE_MOE_H */

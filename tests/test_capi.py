@@ -1,0 +1,194 @@
+"""C-ABI contract tests that need no GPU.
+
+* libcandle_moe_hip.so loads and exports every function include/candle_moe.h
+  declares (the drop-in symbols topk_softmax / fused_moe among them).
+* The host API rejects what the reference's Rust layer rejects, with the
+  reference's error text (/root/reference/src/lib.rs:47-94, 184-242), before
+  any HIP call; the added checks (contiguity, top-k <= E, Qwen3 without down)
+  have their own text.
+* The raw symbols' status variants reject invalid sizes without launching.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import candle_moe as cm
+from candle_moe import DT_BF16, DT_F16, DT_F32, DT_I64, DT_U32, spec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "candle_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    names = header_functions()
+    assert {"topk_softmax", "fused_moe", "candle_moe_fused_moe_status"} <= set(names)
+    L = cm.lib()
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/candle_moe.h but not exported"
+    assert cm.version().startswith("candle-moe-hip")
+
+
+def test_header_symbols_match_reference_ffi_signature():
+    # argument order of /root/reference/src/ffi.rs:15-24 and :45-62
+    src = open(os.path.join(ROOT, "include", "candle_moe.h")).read()
+    topk = re.search(r"void topk_softmax\((.*?)\);", src, re.S).group(1)
+    assert [a.split()[-1].strip("*") for a in topk.split(",")] == [
+        "gating_output", "topk_weight", "topk_indices", "token_expert_indices", "num_experts", "num_tokens",
+        "topk", "stream"]
+    moe = re.search(r"void fused_moe\((.*?)\);", src, re.S).group(1)
+    assert [a.split()[-1].strip("*") for a in moe.split(",")] == [
+        "input", "gate_weights", "up_weights", "down_weights", "routing_weights", "expert_indices", "output",
+        "num_tokens", "hidden_dim", "intermediate_dim", "num_experts", "num_selected_experts", "activation_type",
+        "moe_type", "dtype", "stream"]
+
+
+# ---------------------------------------------------------------- router
+def topk_specs(T=8, E=4, k=2, gdt=DT_F32, wdt=DT_F32, idt=DT_U32, dev=0):
+    return spec((T, E), gdt, dev), spec((T, k), wdt, dev), spec((T, k), idt, dev), spec((T, k), idt, dev)
+
+
+def topk_err(*specs):
+    with pytest.raises(cm.CandleMoeError) as e:
+        cm.validate_topk_softmax(*specs)
+    assert e.value.code == cm.CANDLE_MOE_ERR_INVALID
+    return str(e.value)
+
+
+def test_topk_valid_specs_pass():
+    cm.validate_topk_softmax(*topk_specs())
+    cm.validate_topk_softmax(*topk_specs(T=32768, E=128, k=8))
+    cm.validate_topk_softmax(*topk_specs(gdt=DT_BF16, wdt=DT_BF16))
+
+
+def test_topk_rejections_mirror_lib_rs():
+    g, w, i, ei = topk_specs()
+    assert "is only supported for f32, f16 and bf16" in topk_err(g, spec((8, 2), DT_I64), i, ei)
+    assert "gating_output must be a cuda tensor" in topk_err(spec((8, 4), DT_F32, -1), w, i, ei)
+    assert "expects input tensors of rank 2" in topk_err(spec((8, 4, 1), DT_F32), w, i, ei)
+    assert "num_experts should be power of 2 and smaller than 256" in topk_err(*topk_specs(E=6))
+    assert "num_experts should be power of 2 and smaller than 256" in topk_err(*topk_specs(E=512))
+    assert "shape mismatch topk_indices" in topk_err(g, w, spec((8, 3), DT_U32), ei)
+    assert "shape mismatch token_expert_indices" in topk_err(g, w, i, spec((7, 2), DT_U32))
+    assert "unexpected dtype for gating_output" in topk_err(spec((8, 4), DT_F16), w, i, ei)
+    assert "unexpected dtype for topk_indices" in topk_err(g, w, spec((8, 2), DT_F32), ei)
+    # added checks (the reference reads out of bounds / ignores strides here)
+    assert "top_k must be in" in topk_err(*topk_specs(E=4, k=5))
+    assert "must be contiguous" in topk_err(spec((8, 4), DT_F32, 0, strides=(8, 1)), w, i, ei)
+    assert "shape mismatch gating_output" in topk_err(spec((9, 4), DT_F32), w, i, ei)
+
+
+def test_topk_status_symbol_rejects_without_launch():
+    L = cm.lib()
+    assert L.candle_moe_topk_softmax_status(None, None, None, None, 8, 16, 9, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "topk must be in" in cm.last_error()
+    assert L.candle_moe_topk_softmax_status(None, None, None, None, 0, 16, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_topk_softmax_status(None, None, None, None, 8, 16, 2, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "null tensor pointer" in cm.last_error()
+    # zero tokens is a no-op
+    assert L.candle_moe_topk_softmax_status(None, None, None, None, 8, 0, 2, None) == cm.CANDLE_MOE_OK
+
+
+# ------------------------------------------------------------- fused MoE
+def moe_specs(T=16, H=64, I=256, E=8, k=2, dt=DT_BF16, qwen3=True, dev=0):
+    x = spec((T, H), dt, dev)
+    g = spec((E, H, I), dt, dev)
+    u = spec((E, H, I), dt, dev)
+    d = spec((E, I, H), dt, dev) if qwen3 else None
+    rw = spec((T, k), DT_F32, dev)
+    ix = spec((T, k), DT_U32, dev)
+    out = spec((T, H), dt, dev)
+    return x, g, u, d, rw, ix, out
+
+
+def moe_err(moe, specs, moe_type=0):
+    x, g, u, d, rw, ix, out = specs
+    with pytest.raises(cm.CandleMoeError) as e:
+        moe.validate(x, g, u, d, rw, ix, moe_type, out)
+    return str(e.value)
+
+
+def test_moe_valid_specs_pass():
+    moe = cm.FusedMoE.new(8, 2, cm.Activation.Silu)
+    x, g, u, d, rw, ix, out = moe_specs()
+    moe.validate(x, g, u, d, rw, ix, 0, out)
+    x, g, u, d, rw, ix, out = moe_specs(qwen3=False, dt=DT_F32)
+    moe.validate(x, g, u, None, rw, ix, 1, out)
+    big = cm.FusedMoE.new(128, 8, cm.Activation.Silu)
+    x, g, u, d, rw, ix, out = moe_specs(T=4096, H=2048, I=768, E=128, k=8)
+    big.validate(x, g, u, d, rw, ix, 0, out)
+
+
+def test_moe_rejections_mirror_lib_rs():
+    moe = cm.FusedMoE.new(8, 2, cm.Activation.Silu)
+    s = list(moe_specs())
+    assert "Number of experts mismatch" in moe_err(cm.FusedMoE.new(4, 2, cm.Activation.Silu), s)
+    t = list(s); t[1] = spec((8, 32, 256), DT_BF16)
+    assert "Hidden dimension mismatch for gate/up weights" in moe_err(moe, t)
+    t = list(s); t[3] = spec((8, 256, 32), DT_BF16)
+    assert "Hidden dimension mismatch for down weights (expected 64, got 32)" in moe_err(moe, t)
+    t = list(s); t[2] = spec((8, 64, 128), DT_BF16)
+    assert "Intermediate dimension mismatch (gate: 256, up: 128, down: 256)" in moe_err(moe, t)
+    t = list(s); t[4] = spec((15, 2), DT_F32)
+    assert "Number of tokens mismatch" in moe_err(moe, t)
+    t = list(s); t[5] = spec((16, 3), DT_U32)
+    assert "Number of selected experts mismatch" in moe_err(moe, t)
+    assert "moe_type must be one of 0 or 1" in moe_err(moe, s, moe_type=2)
+    t = [spec(tuple(a.dims[: a.rank]), DT_I64) if a is not None else None for a in s]
+    t[4], t[5] = s[4], s[5]
+    assert "FusedMoE is only supported for f16, bf16 and f32" in moe_err(moe, t)
+    t = list(s); t[0] = spec((16, 64), DT_BF16, -1)
+    assert "input must be a cuda tensor" in moe_err(moe, t)
+    t = list(s); t[4] = spec((16, 2), DT_BF16)
+    assert "unexpected dtype for routing_weights, expected: F32" in moe_err(moe, t)
+    t = list(s); t[5] = spec((16, 2), DT_I64)
+    assert "unexpected dtype for expert_indices, expected: U32" in moe_err(moe, t)
+    t = list(s); t[1] = spec((8, 64, 256), DT_F16)
+    assert "unexpected dtype for gate_weights" in moe_err(moe, t)
+    t = list(s); t[0] = spec((16, 64, 1), DT_BF16)
+    assert "unexpected rank, expected: 2" in moe_err(moe, t)
+
+
+def test_moe_added_checks():
+    moe = cm.FusedMoE.new(8, 2, cm.Activation.Silu)
+    s = list(moe_specs())
+    t = list(s); t[3] = None
+    assert "down_weights is required for moe_type 0" in moe_err(moe, t, moe_type=0)
+    t = list(s); t[1] = spec((8, 64, 256), DT_BF16, 0, strides=(16384, 1, 64))
+    assert "gate_weights must be contiguous" in moe_err(moe, t)
+    t = list(s); t[6] = spec((16, 32), DT_BF16)
+    assert "shape mismatch output" in moe_err(moe, t)
+
+
+def test_moe_status_symbol_rejects_without_launch():
+    L = cm.lib()
+    args = [None] * 7
+    assert L.candle_moe_fused_moe_status(*args, 16, 64, 256, 8, 2, 0, 2, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "moe_type must be one of 0 or 1" in cm.last_error()
+    assert L.candle_moe_fused_moe_status(*args, 16, 64, 256, 8, 2, 5, 0, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "activation_type" in cm.last_error()
+    assert L.candle_moe_fused_moe_status(*args, 16, 64, 256, 8, 2, 0, 0, 3, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_fused_moe_status(*args, 16, 64, 256, 8, 2, 0, 0, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "null tensor pointer" in cm.last_error()
+    assert L.candle_moe_fused_moe_status(*args, 0, 64, 256, 8, 2, 0, 0, 1, None) == cm.CANDLE_MOE_OK
+
+
+def test_workspace_size():
+    L = cm.lib()
+    small = L.candle_moe_fused_moe_workspace_size(32, 64, 256, 8, 2, 1)
+    big = L.candle_moe_fused_moe_workspace_size(32768, 4096, 1536, 8, 2, 1)
+    assert 0 < small < big
+    # holds at least the bf16 intermediate [T*k, I] and the f32 accumulator [T, H]
+    assert big >= 65536 * 1536 * 2 + 32768 * 4096 * 4
+    assert L.candle_moe_fused_moe_workspace_size(32, 64, 256, 0, 2, 1) == 0
+    # workspace variant: too-small workspace is refused before anything runs
+    rc = L.candle_moe_fused_moe_ws(*([ctypes.c_void_p(256)] * 7), 32, 64, 256, 8, 2, 0, 0, 1,
+                                   ctypes.c_void_p(256), 16, None)
+    assert rc == cm.CANDLE_MOE_ERR_WORKSPACE

@@ -1,0 +1,196 @@
+"""Fused-MoE parity on the GPU: HIP kernels vs the CPU oracle.
+
+Tolerances (north star): rtol 1e-4 (f32), 1e-2 (f16), 2e-2 (bf16) with
+atol = rtol * RMS(expected), in the reference's |a-b| <= atol + rtol*max
+form (/root/reference/tests/moe_tests.rs:61-91). The GPU result is checked
+against both oracle modes: the candle-native per-op rounding and the f64
+evaluation of the same dtype-valued inputs.
+"""
+import ctypes
+import zlib
+
+import numpy as np
+import pytest
+
+import candle_moe
+import oracle as O
+from helpers import RTOL, assert_close, assert_close_norm, from_dev, moe_inputs, to_dev
+
+pytestmark = pytest.mark.gpu
+
+ACT = {O.SILU: candle_moe.Activation.Silu, O.GELU: candle_moe.Activation.Gelu, O.RELU: candle_moe.Activation.Relu}
+
+
+def run_moe(x, G, U, D, rw, ri, E, k, act, moe_type, dt):
+    import torch
+
+    moe = candle_moe.FusedMoE.new(E, k, ACT[act])
+    out = moe.forward(to_dev(x, dt), to_dev(G, dt), to_dev(U, dt), None if D is None else to_dev(D, dt),
+                      to_dev(rw), to_dev(ri), moe_type)
+    torch.cuda.synchronize()
+    return from_dev(out).astype(np.float64)
+
+
+def run_raw(x, G, U, D, rw, ri, E, k, act, moe_type, dt, out_init=None, workspace=False):
+    """Through the reference's fused_moe symbol (or its workspace variant)."""
+    import torch
+
+    T, H = x.shape
+    I = G.shape[2]
+    tx, tg, tu = to_dev(x, dt), to_dev(G, dt), to_dev(U, dt)
+    td = None if D is None else to_dev(D, dt)
+    trw, tri = to_dev(rw), to_dev(ri)
+    if out_init is None:
+        out = torch.zeros((T, H), dtype=tx.dtype, device="cuda:0")
+    else:
+        out = torch.from_numpy(out_init.astype(np.float32)).to("cuda:0").to(tx.dtype)
+    L = candle_moe.lib()
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if workspace:
+        n = L.candle_moe_fused_moe_workspace_size(T, H, I, E, k, dt)
+        ws = torch.empty(n + 256, dtype=torch.uint8, device="cuda:0")
+        base = (ws.data_ptr() + 255) // 256 * 256
+        rc = L.candle_moe_fused_moe_ws(p(tx), p(tg), p(tu), p(td), p(trw), p(tri), p(out), T, H, I, E, k, act,
+                                       moe_type, dt, ctypes.c_void_p(base), n, stream)
+        candle_moe.check(rc)
+    else:
+        L.fused_moe(p(tx), p(tg), p(tu), p(td), p(trw), p(tri), p(out), T, H, I, E, k, act, moe_type, dt, stream)
+        assert candle_moe.last_error() == "", candle_moe.last_error()
+    torch.cuda.synchronize()
+    return from_dev(out).astype(np.float64)
+
+
+def check_case(T, H, I, E, k, dt, moe_type, act=O.SILU, seed=0, wstd=0.02, rows=None, skew=0.0, zipf=0.0,
+               api="host"):
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, seed, moe_type, wstd=wstd, skew_sigma=skew, zipf_s=zipf)
+    if api == "host":
+        got = run_moe(x, G, U, D, rw, ri, E, k, act, moe_type, dt)
+    else:
+        got = run_raw(x, G, U, D, rw, ri, E, k, act, moe_type, dt, workspace=(api == "ws"))
+    kw = dict(E=E, k=k, act=act, moe_type=moe_type, dtype=dt, rows=rows)
+    f32acc = O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_F32ACC, **kw)
+    exact = O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_EXACT, **kw)
+    cand = O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_CANDLE, **kw)
+    if rows is not None:
+        got = got[np.asarray(rows)]
+    name = f"T={T} H={H} I={I} E={E} k={k} dt={dt} type={moe_type} act={act}"
+    assert_close(got, f32acc, RTOL[dt], name + " vs f32-accumulation oracle")
+    assert_close(got, exact, RTOL[dt], name + " vs f64 oracle")
+    assert_close_norm(got, cand, RTOL[dt], name + " vs candle per-op-rounding oracle")
+    return got
+
+
+# ---- the reference's own test cases (/root/reference/tests/moe_tests.rs:279-397):
+# E=8, SiLU, I = 4H, weights N(0,1)
+REF_CASES = [
+    ("nomic_fp32", O.F32, 16, 16, 2, O.NOMIC),
+    ("nomic_fp16_gemm", O.F16, 64, 32, 2, O.NOMIC),
+    ("nomic_fp16_gemm_topk1", O.F16, 64, 32, 1, O.NOMIC),
+    ("qwen3_fp32", O.F32, 64, 32, 2, O.QWEN3),
+    ("qwen3_fp16_direct", O.F16, 64, 4, 2, O.QWEN3),
+    ("qwen3_fp16_gemm", O.F16, 64, 32, 2, O.QWEN3),
+    ("qwen3_fp16_gemm_topk1", O.F16, 64, 32, 1, O.QWEN3),
+    ("qwen3_bf16_direct", O.BF16, 64, 4, 2, O.QWEN3),
+    ("qwen3_bf16_gemm", O.BF16, 64, 32, 2, O.QWEN3),
+    ("qwen3_bf16_gemm_topk1", O.BF16, 64, 32, 1, O.QWEN3),
+]
+
+
+@pytest.mark.parametrize("name,dt,H,T,k,mt", REF_CASES, ids=[c[0] for c in REF_CASES])
+def test_reference_cases(name, dt, H, T, k, mt):
+    check_case(T, H, 4 * H, 8, k, dt, mt, wstd=1.0, seed=zlib.crc32(name.encode()) % 1000)
+
+
+# ---- BASELINE config 3 (Nomic, H768 I3072 E8 k2 GELU) at the sizes the oracle finishes quickly
+@pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
+@pytest.mark.parametrize("T", [16, 64])
+def test_nomic_config(dt, T):
+    check_case(T, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=3)
+
+
+# ---- BASELINE config 4 (Qwen3, H4096 I1536 E8 k2 SiLU)
+@pytest.mark.parametrize("dt", [O.F16, O.BF16])
+@pytest.mark.parametrize("T", [8, 16, 32, 64])
+def test_qwen3_config(dt, T):
+    check_case(T, 4096, 1536, 8, 2, dt, O.QWEN3, seed=4)
+
+
+# ---- BASELINE config 5 (Qwen3-30B-A3B: H2048 I768 E128 k8, Zipf-skewed routing)
+@pytest.mark.parametrize("T", [1, 16, 128])
+def test_qwen3_30b_config(T):
+    check_case(T, 2048, 768, 128, 8, O.BF16, O.QWEN3, seed=5, zipf=1.1)
+
+
+def test_activations_and_odd_shapes():
+    for act in (O.SILU, O.GELU, O.RELU):
+        check_case(40, 96, 72, 4, 2, O.BF16, O.QWEN3, act=act, seed=6)
+        check_case(40, 96, 72, 4, 2, O.F32, O.NOMIC, act=act, seed=7)
+    # shapes that are not multiples of 8 take the SIMT kernels
+    check_case(19, 20, 36, 3, 2, O.BF16, O.QWEN3, seed=8)
+    check_case(19, 20, 36, 3, 3, O.F16, O.NOMIC, seed=9)
+
+
+def test_raw_symbol_and_workspace_variant():
+    a = check_case(48, 256, 128, 8, 2, O.BF16, O.QWEN3, seed=10, api="raw")
+    b = check_case(48, 256, 128, 8, 2, O.BF16, O.QWEN3, seed=10, api="ws")
+    assert np.array_equal(a, b)
+
+
+def test_output_is_accumulated():
+    # the reference kernels add into the caller's output (ffi.rs:35 requires zeros)
+    T, H, I, E, k = 32, 128, 64, 4, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 11, O.QWEN3)
+    init = O.round_to(O.randn((T, H), seed=12), O.BF16).astype(np.float64)
+    got = run_raw(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init)
+    want = O.fused_moe(x, G, U, D, rw, ri, E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16,
+                       mode=O.MODE_EXACT) + init
+    assert_close(got, want, RTOL[O.BF16], "accumulate into output")
+
+
+def test_empty_and_invalid_indices():
+    import torch
+
+    moe = candle_moe.FusedMoE.new(4, 2, candle_moe.Activation.Silu)
+    x = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda:0")
+    g = torch.zeros((4, 64, 32), dtype=torch.bfloat16, device="cuda:0")
+    d = torch.zeros((4, 32, 64), dtype=torch.bfloat16, device="cuda:0")
+    rw = torch.zeros((0, 2), dtype=torch.float32, device="cuda:0")
+    ri = torch.zeros((0, 2), dtype=torch.int32, device="cuda:0")
+    out = moe.forward(x, g, g, d, rw, ri, 0)
+    assert out.shape == (0, 64)
+    # expert ids >= E are dropped (/root/reference/kernels/preprocessing.cuh:49-52)
+    T, H, I, E, k = 16, 64, 32, 4, 2
+    xx, G, U, D, w, i = moe_inputs(T, H, I, E, k, O.BF16, 13, O.QWEN3)
+    i = i.copy()
+    i[::3, 1] = 99
+    got = run_moe(xx, G, U, D, w, i, E, k, O.SILU, O.QWEN3, O.BF16)
+    want = O.fused_moe(xx, G, U, D, w, i, E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16, mode=O.MODE_EXACT)
+    assert_close(got, want, RTOL[O.BF16], "dropped pairs")
+
+
+def test_deterministic_k2():
+    x, G, U, D, rw, ri = moe_inputs(512, 1024, 512, 8, 2, O.BF16, 14, O.QWEN3)
+    a = run_moe(x, G, U, D, rw, ri, 8, 2, O.SILU, O.QWEN3, O.BF16)
+    b = run_moe(x, G, U, D, rw, ri, 8, 2, O.SILU, O.QWEN3, O.BF16)
+    assert np.array_equal(a, b)
+
+
+# ---- full BASELINE sizes, checked on a sample of tokens (each output row
+# depends only on its own token, its routing and the weights)
+SAMPLE = [0, 1, 2, 777, 4095, 5000, 12345, 20000, 32767]
+
+
+@pytest.mark.slow
+def test_qwen3_full_size_sampled():
+    check_case(32768, 4096, 1536, 8, 2, O.BF16, O.QWEN3, seed=15, rows=SAMPLE)
+
+
+@pytest.mark.slow
+def test_nomic_full_size_sampled():
+    check_case(32768, 768, 3072, 8, 2, O.BF16, O.NOMIC, act=O.GELU, seed=16, rows=SAMPLE)
+
+
+@pytest.mark.slow
+def test_qwen3_30b_prefill_sampled():
+    check_case(4096, 2048, 768, 128, 8, O.BF16, O.QWEN3, seed=17, zipf=1.1, rows=[0, 1, 100, 2047, 4095])
