@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the candle-moe hot path on one MI355X.
+
+Metric: fused-MoE µs & TFLOP/s (Qwen3 h4096 E8 k2 bf16);
+topk-softmax µs. One step = one MoE layer over one batch of synthetic
+tokens already resident in HBM: topk-softmax over the router logits
+[T, E], then FusedMoE::forward (zeroed output, grouping, gate/up GEMM with
+SwiGLU, down GEMM with the weighted combine). Default workload: Qwen3
+T=32768, H=4096, I=1536, E=8, k=2, bf16 (BASELINE config 4 at its largest T).
+
+Prints ONE JSON line. `value` is TFLOP/s of the whole step (algorithmic
+MoE FLOPs = T*k*6*H*I for Qwen3, T*k*4*H*I for Nomic). `roofline` is for the
+dominant kernel (the gate/up GEMM), timed with HIP events on the stream it
+runs on (candle_moe_profile_*). `cpu_baseline` times the CPU oracle (the
+candle-native per-expert loop, a port) on a bounded token sample.
+
+    python bench.py [--steps K] [--warmup W] [--workload qwen3|nomic|q30b|router]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "candle-moe_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/f16 MFMA
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # BASELINE config 4 (headline): Qwen3 SwiGLU
+    "qwen3": dict(T=32768, H=4096, I=1536, E=8, k=2, moe_type=0, act="silu", dtype="bf16", zipf=0.0),
+    # Nomic fc1 -> GELU -> fc2
+    "nomic": dict(T=32768, H=768, I=3072, E=8, k=2, moe_type=1, act="gelu", dtype="bf16", zipf=0.0),
+    # Qwen3-30B-A3B-shaped, Zipf-skewed routing
+    "q30b": dict(T=4096, H=2048, I=768, E=128, k=8, moe_type=0, act="silu", dtype="bf16", zipf=1.1),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + ["router"])
+    ap.add_argument("--tokens", type=int, default=0, help="override T")
+    ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-sample", type=int, default=2048, help="tokens in the CPU-baseline sample (0 = skip)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the hot path is a single-device kernel "
+                                   "set; run with --gpus 1 (sharding design: DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    import candle_moe as cm
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = cm.lib()
+
+    if args.workload == "router":
+        return bench_router_only(args, torch, cm, dev)
+
+    wl = dict(WORKLOADS[args.workload])
+    if args.tokens:
+        wl["T"] = args.tokens
+    if args.dtype:
+        wl["dtype"] = args.dtype
+    T, H, I, E, k = wl["T"], wl["H"], wl["I"], wl["E"], wl["k"]
+    qwen3 = wl["moe_type"] == 0
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[wl["dtype"]]
+    act = {"silu": cm.Activation.Silu, "gelu": cm.Activation.Gelu, "relu": cm.Activation.Relu}[wl["act"]]
+
+    # synthetic inputs (torch's seeded GPU generator), weights N(0, 0.02) in the API layout
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    x = torch.randn((T, H), generator=g, device=dev).to(tdt)
+    gate = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(tdt)
+    up = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(tdt)
+    down = (torch.randn((E, I, H), generator=g, device=dev) * 0.02).to(tdt) if qwen3 else None
+    logits = torch.randn((T, E), generator=g, device=dev)
+    if wl["zipf"]:
+        ranks = torch.randperm(E, generator=torch.Generator().manual_seed(args.seed)).double() + 1
+        p = ranks ** (-wl["zipf"])
+        logits += torch.log(p / p.sum()).float().to(dev)[None, :]
+    topk_w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    topk_i = torch.empty((T, k), dtype=torch.int32, device=dev)
+    tok_ei = torch.empty((T, k), dtype=torch.int32, device=dev)
+    moe = cm.FusedMoE.new(E, k, act)
+    torch.cuda.synchronize()
+
+    def step():
+        cm.apply_topk_softmax_inplace(logits, topk_w, topk_i, tok_ei)
+        return moe.forward(x, gate, up, down, topk_w, topk_i, wl["moe_type"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    nslots = L.candle_moe_profile_begin()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (ctypes.c_double * nslots)()
+    cnt = (ctypes.c_int * nslots)()
+    cm.check(L.candle_moe_profile_end(ms, cnt, nslots))
+    L.candle_moe_profile_slot_name.restype = ctypes.c_char_p
+    kernels = {}
+    for s in range(nslots):
+        if cnt[s]:
+            kernels[L.candle_moe_profile_slot_name(s).decode()] = round(1000.0 * ms[s] / cnt[s], 3)
+
+    ms_per_step = (t1 - t0) * 1000.0 / args.steps
+    c = 6 if qwen3 else 4
+    flops = float(T) * k * c * H * I
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    peak = PEAK_F32_TFLOPS if wl["dtype"] == "f32" else PEAK_BF16_TFLOPS
+
+    # dominant kernel: gate/up (Qwen3: x.[G|U], 2*P*H*2I flops) or fc1 (Nomic: 2*P*H*I)
+    g1_us = kernels.get("gemm_gate_up", 0.0)
+    g1_flops = float(T) * k * (4 if qwen3 else 2) * H * I
+    g1_achieved = g1_flops / (g1_us * 1e-6) / 1e12 if g1_us else 0.0
+    topk_us = kernels.get("topk_softmax", 0.0)
+    topk_bytes = T * E * 4 + T * k * 12
+    traffic = load_traffic(args.workload, wl)
+
+    cpu = None
+    if args.cpu_sample > 0:
+        cpu = cpu_baseline(torch, x, gate, up, down, topk_w, topk_i, wl, min(args.cpu_sample, T))
+
+    line = {
+        "metric": "fused-MoE µs & TFLOP/s (Qwen3 h4096 E8 k2 bf16); topk-softmax µs",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": "synthetic (torch seeded GPU RNG: x ~ N(0,1), weights ~ N(0,0.02), logits ~ N(0,1))",
+        "config": {
+            "workload": f"{args.workload}-moe layer: topk-softmax [{T},{E}] k={k} + fused MoE T={T} H={H} I={I} "
+                        f"E={E} k={k} {'SwiGLU' if qwen3 else 'fc1-' + wl['act'] + '-fc2'} {wl['dtype']}",
+            "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
+            "moe_type": wl["moe_type"], "activation": wl["act"], "zipf_bias": wl["zipf"], "seed": args.seed,
+            "parallelism": "single GPU",
+        },
+        "fused_moe_us": round(1000.0 * ms_per_step - topk_us, 1),
+        "topk_softmax_us": topk_us,
+        "topk_softmax_gbs": round(topk_bytes / (topk_us * 1e-6) / 1e9, 1) if topk_us else None,
+        "kernels_us": kernels,
+        "roofline": {
+            "kernel": "gemm_gate_up" if qwen3 else "gemm_fc1",
+            "bound": "mfma",
+            "achieved": round(g1_achieved, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(g1_achieved / peak, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    del out
+
+
+def load_traffic(workload, wl):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (profiles/traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        rec = d.get(workload)
+        if rec and rec.get("tokens") == wl["T"]:
+            return rec.get("bytes_per_launch")
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def cpu_baseline(torch, x, gate, up, down, topk_w, topk_i, wl, S):
+    """CPU oracle (candle-native per-expert loop, bf16 per-op rounding, f32
+    matmul accumulation) on the first S tokens with all weights."""
+    import numpy as np
+
+    import oracle as O
+
+    dt = {"bf16": O.BF16, "f16": O.F16, "f32": O.F32}[wl["dtype"]]
+
+    def host(t):
+        if t is None:
+            return None
+        t = t.contiguous().cpu()
+        if t.dtype in (torch.bfloat16, torch.float16):
+            return t.view(torch.int16).numpy().view(np.uint16)
+        return t.numpy()
+
+    xs = host(x[:S])
+    G, U, D = host(gate), host(up), host(down)
+    w = topk_w[:S].cpu().numpy()
+    idx = topk_i[:S].cpu().numpy().astype(np.uint32)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    act = {"silu": O.SILU, "gelu": O.GELU, "relu": O.RELU}[wl["act"]]
+    t0 = time.perf_counter()
+    O.fused_moe(xs, G, U, D, w, idx, E=wl["E"], k=wl["k"], act=act, moe_type=wl["moe_type"], dtype=dt,
+                mode=O.MODE_CANDLE, nthreads=threads)
+    dt_s = time.perf_counter() - t0
+    c = 6 if wl["moe_type"] == 0 else 4
+    flops = float(S) * wl["k"] * c * wl["H"] * wl["I"]
+    return {
+        "value": round(flops / dt_s / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first {S} of {wl['T']} tokens with all {wl['E']} experts' weights; candle-native "
+                  f"per-expert loop (oracle/oracle.c, per-op {wl['dtype']} rounding); {dt_s:.2f} s wall",
+    }
+
+
+def bench_router_only(args, torch, cm, dev):
+    """topk-softmax alone over BASELINE config 2 shapes (µs and GB/s)."""
+    L = cm.lib()
+    res = {}
+    for (T, E, k) in [(32768, 8, 2), (32768, 64, 6), (32768, 128, 8)]:
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed)
+        # rotate over enough logits buffers to exceed the 256 MB last-level cache
+        nbuf = max(1, (512 << 20) // (T * E * 4))
+        logits = [torch.randn((T, E), generator=g, device=dev) for _ in range(nbuf)]
+        w = torch.empty((T, k), device=dev)
+        i = torch.empty((T, k), dtype=torch.int32, device=dev)
+        ei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        for _ in range(args.warmup):
+            cm.apply_topk_softmax_inplace(logits[0], w, i, ei)
+        torch.cuda.synchronize()
+        n = L.candle_moe_profile_begin()
+        for s in range(max(args.steps, 50)):
+            cm.apply_topk_softmax_inplace(logits[s % nbuf], w, i, ei)
+        torch.cuda.synchronize()
+        ms = (ctypes.c_double * n)()
+        cnt = (ctypes.c_int * n)()
+        cm.check(L.candle_moe_profile_end(ms, cnt, n))
+        us = 1000.0 * ms[0] / cnt[0]
+        nbytes = T * E * 4 + T * k * 12
+        res[f"{T}x{E}k{k}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    head = res["32768x8k2"]
+    print(json.dumps({
+        "metric": "topk-softmax µs", "value": head["us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["us"] / 1000.0, "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic N(0,1) logits, cold buffers",
+        "config": {"workload": "topk-softmax [32768,E] (config 2)"}, "shapes": res,
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }))
+
+
+if __name__ == "__main__":
+    main()

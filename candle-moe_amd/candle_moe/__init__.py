@@ -100,6 +100,16 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_workspace_size.restype = sz
         L.candle_moe_fused_moe_ws.argtypes = moe_args + [vp, sz, vp]
         L.candle_moe_fused_moe_ws.restype = i32
+        L.candle_moe_set_combine_policy.argtypes = [i32]
+        L.candle_moe_set_combine_policy.restype = i32
+        L.candle_moe_fused_moe_path.argtypes = [i32] * 5 + [u32]
+        L.candle_moe_fused_moe_path.restype = i32
+        L.candle_moe_profile_begin.argtypes = []
+        L.candle_moe_profile_begin.restype = i32
+        L.candle_moe_profile_end.argtypes = [vp, vp, i32]
+        L.candle_moe_profile_end.restype = i32
+        L.candle_moe_profile_slot_name.argtypes = [i32]
+        L.candle_moe_profile_slot_name.restype = ctypes.c_char_p
         L.candle_moe_last_error.argtypes = []
         L.candle_moe_last_error.restype = ctypes.c_char_p
         L.candle_moe_version.argtypes = []
@@ -258,7 +268,22 @@ def version() -> str:
     return lib().candle_moe_version().decode()
 
 
+COMBINE_AUTO, COMBINE_PAIRS, COMBINE_EXPERT_SETS = 0, 1, 2
+PATH_NAMES = {2: "expert-set", 1: "pairs", 0: "simt", -1: "invalid"}
+
+
+def set_combine_policy(policy: int) -> None:
+    """Process-wide fused_moe combine strategy (COMBINE_*; default auto)."""
+    check(lib().candle_moe_set_combine_policy(int(policy)))
+
+
+def fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> str:
+    """Name of the path fused_moe takes for these sizes under the current policy."""
+    return PATH_NAMES[lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k,
+                                                      dtype_code)]
+
+
 __all__ = [
     "Activation", "FusedMoE", "apply_topk_softmax_inplace", "CandleMoeError", "lib", "describe", "spec",
-    "validate_topk_softmax", "version", "LIB_PATH",
+    "validate_topk_softmax", "version", "LIB_PATH", "set_combine_policy", "fused_moe_path",
 ]

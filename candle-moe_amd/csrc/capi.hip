@@ -2,10 +2,15 @@
 // (/root/reference/src/ffi.rs:15-62), their status-returning variants and
 // the fused-MoE dispatcher (/root/reference/kernels/moe.cu:453-771).
 //
-// Dispatcher, per call, all on the caller's stream, no host sync:
-//   grouping (3 launches) -> GEMM1 (gate+up or fc1, activation fused)
-//   -> zero f32 accumulator -> GEMM2 (down or fc2, routing weight and
-//   scatter-add fused) -> finalize (output += accumulator, rounded once).
+// Dispatcher, per call, all on the caller's stream, no host sync. Two paths:
+//  expert-set path (few distinct expert sets next to the token count):
+//   pair grouping + token grouping by expert set -> GEMM1 (gate+up or fc1,
+//   activation and routing weight fused, rows written in token-set order)
+//   -> GEMM2 over K = k*I per expert set, added once into the output.
+//  pair path (everything else):
+//   pair grouping -> GEMM1 (activation fused) -> zero f32 accumulator
+//   -> GEMM2 (routing weight and coalesced f32 atomic scatter-add fused)
+//   -> finalize (output += accumulator, rounded once).
 // Workspace (256-byte aligned pieces): offsets[E+2], per-block counts,
 // sorted pair ids, row-tile table, intermediate [T*k, I] in the input dtype
 // and the f32 accumulator [T, H].
@@ -14,6 +19,7 @@
 
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/candle_moe.h"
 #include "cm_common.hpp"
@@ -39,6 +45,40 @@ static int hip_fail(hipError_t e, const char* what) {
     return set_error(CANDLE_MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// ------------------------------------------------------------- profiling
+// Optional per-kernel timing: while enabled, every internal launch is
+// bracketed by a pair of HIP events on the caller's stream.
+enum ProfSlot { kSlotTopk = 0, kSlotGroup, kSlotGemm1, kSlotZero, kSlotGemm2, kSlotFinal, kNumSlots };
+static const char* kSlotNames[kNumSlots] = {"topk_softmax", "grouping", "gemm_gate_up", "acc_clear",
+                                            "gemm_down", "finalize"};
+struct ProfRec {
+    int slot;
+    hipEvent_t a, b;
+};
+static std::mutex g_prof_mu;
+static bool g_prof_on = false;
+static std::vector<ProfRec> g_prof;
+
+struct ProfScope {
+    ProfRec rec;
+    hipStream_t s;
+    bool on;
+    ProfScope(int slot, hipStream_t stream) : s(stream), on(false) {
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        if (!g_prof_on) return;
+        rec.slot = slot;
+        if (hipEventCreate(&rec.a) != hipSuccess) return;
+        if (hipEventCreate(&rec.b) != hipSuccess) { (void)hipEventDestroy(rec.a); return; }
+        on = hipEventRecord(rec.a, s) == hipSuccess;
+    }
+    ~ProfScope() {
+        if (!on) return;
+        (void)hipEventRecord(rec.b, s);
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        g_prof.push_back(rec);
+    }
+};
+
 // ------------------------------------------------------------------ router
 int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void* ei, int E, int T, int k,
                       void* stream) {
@@ -50,9 +90,12 @@ int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void*
         return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: topk must be in [1, num_experts=%d] (got %d)", E, k);
     if (T == 0) return CANDLE_MOE_OK;
     if (!g || !w || !idx || !ei) return set_error(CANDLE_MOE_ERR_INVALID, "topk_softmax: null tensor pointer");
-    const hipError_t e = launch_topk_softmax(g, gdt, w, wdt, reinterpret_cast<uint32_t*>(idx),
-                                             reinterpret_cast<uint32_t*>(ei), T, E, k,
-                                             reinterpret_cast<hipStream_t>(stream));
+    hipError_t e;
+    {
+        ProfScope ps(kSlotTopk, reinterpret_cast<hipStream_t>(stream));
+        e = launch_topk_softmax(g, gdt, w, wdt, reinterpret_cast<uint32_t*>(idx), reinterpret_cast<uint32_t*>(ei), T,
+                                E, k, reinterpret_cast<hipStream_t>(stream));
+    }
     if (e == hipErrorInvalidValue && !((gdt == wdt) || wdt == kF32))
         return set_error(CANDLE_MOE_ERR_UNSUPPORTED, "topk_softmax: unsupported dtype pair (%d, %d)", gdt, wdt);
     if (e != hipSuccess) return hip_fail(e, "topk_softmax launch");
@@ -65,11 +108,23 @@ struct Problem {
     bool mfma;
     int BM;
     long long P;
+    bool set_path;  // expert-set down projection (no atomics, no f32 accumulator)
+    int nkeys;      // (E+1)^k expert-set keys
 };
 
 struct Layout {
-    size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles, inter, acc, total;
+    size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles;
+    size_t k_offsets, k_block_counts, tok_sorted, tile_row2, tile_key2, num_tiles2, pair_dest;
+    size_t inter, acc, total;
 };
+
+// 0: choose per call; 1: always the pair path (f32 atomics); 2: the
+// expert-set path whenever the shape allows it.
+static int g_combine_policy = 0;
+
+static long long set_tiles_max(const Problem& p) {
+    return (p.T + p.BM - 1) / p.BM + (p.nkeys < p.T ? p.nkeys : p.T);
+}
 
 static size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -85,8 +140,22 @@ static Layout make_layout(const Problem& p) {
     L.tile_row = o; o += a256((size_t)mt * 4);
     L.tile_exp = o; o += a256((size_t)mt * 4);
     L.num_tiles = o; o += 256;
+    if (p.set_path) {
+        const long long nbt = grouping_blocks(p.T);
+        const long long mt2 = set_tiles_max(p);
+        L.k_offsets = o; o += a256((size_t)(p.nkeys + 2) * 4);
+        L.k_block_counts = o; o += a256((size_t)(nbt > 0 ? nbt : 1) * p.nkeys * 4);
+        L.tok_sorted = o; o += a256((size_t)(p.T > 0 ? p.T : 1) * 4);
+        L.tile_row2 = o; o += a256((size_t)mt2 * 4);
+        L.tile_key2 = o; o += a256((size_t)mt2 * 4);
+        L.num_tiles2 = o; o += 256;
+        L.pair_dest = o; o += a256((size_t)(p.P > 0 ? p.P : 1) * 4);
+    } else {
+        L.k_offsets = L.k_block_counts = L.tok_sorted = L.tile_row2 = L.tile_key2 = L.num_tiles2 = L.pair_dest = 0;
+    }
     L.inter = o; o += a256((size_t)p.P * p.I * es);
-    L.acc = o; o += a256((size_t)p.T * p.H * 4);
+    L.acc = o;
+    if (!p.set_path) o += a256((size_t)p.T * p.H * 4);
     L.total = o;
     return L;
 }
@@ -109,6 +178,22 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.P = P;
     p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
     p.BM = p.mfma ? kMfmaBM : kSimtBM;
+    // Expert-set path: each distinct sorted expert set becomes one GEMM group
+    // over K = k*I; worth it when the sets are few next to the tokens (on
+    // average at least half a row tile per set, e.g. E=8, k=2 from T >= 1792).
+    p.set_path = false;
+    p.nkeys = 0;
+    if (p.mfma && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
+        long long nk = 1;
+        for (int j = 0; j < k && nk <= kSetMaxKeys; ++j) nk *= (E + 1);
+        if (nk <= kSetMaxKeys) {
+            double sets = 1.0;
+            for (int j = 0; j < k; ++j) sets = sets * (E - j) / (j + 1);
+            if (sets < 1.0) sets = 1.0;
+            p.nkeys = (int)nk;
+            p.set_path = g_combine_policy == 2 || (double)T >= 0.5 * kMfmaBM * sets;
+        }
+    }
     return CANDLE_MOE_OK;
 }
 
@@ -122,13 +207,33 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     gb.tile_row = reinterpret_cast<int32_t*>(ws + L.tile_row);
     gb.tile_exp = reinterpret_cast<int32_t*>(ws + L.tile_exp);
     gb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles);
-    hipError_t e = launch_grouping(idx, p.P, p.E, p.BM, gb, s);
+    hipError_t e;
+    {
+        ProfScope ps(kSlotGroup, s);
+        e = launch_grouping(idx, p.P, p.E, p.BM, gb, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "fused_moe grouping");
 
     const bool qwen3 = p.moe_type == kQwen3;
     const int m_tiles_max = (int)grouping_max_tiles(p.P, p.E, p.BM);
     void* inter = ws + L.inter;
     float* acc = reinterpret_cast<float*>(ws + L.acc);
+    GroupingBufs tb = {};
+    int32_t* pair_dest = nullptr;
+    if (p.set_path) {
+        tb.offsets = reinterpret_cast<int32_t*>(ws + L.k_offsets);
+        tb.block_counts = reinterpret_cast<int32_t*>(ws + L.k_block_counts);
+        tb.sorted_pair = reinterpret_cast<int32_t*>(ws + L.tok_sorted);
+        tb.tile_row = reinterpret_cast<int32_t*>(ws + L.tile_row2);
+        tb.tile_exp = reinterpret_cast<int32_t*>(ws + L.tile_key2);
+        tb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles2);
+        pair_dest = reinterpret_cast<int32_t*>(ws + L.pair_dest);
+        {
+            ProfScope ps(kSlotGroup, s);
+            e = launch_token_grouping(idx, p.T, p.k, p.E, p.nkeys, p.BM, tb, pair_dest, s);
+        }
+        if (e != hipSuccess) return hip_fail(e, "fused_moe expert-set grouping");
+    }
 
     GemmArgs g1 = {};
     g1.A = x;
@@ -150,10 +255,49 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     const int mode1 = qwen3 ? kGateUp : kFc1;
     g1.n_tiles = cdiv(p.I, gemm_tile_cols(mode1, p.mfma));
     g1.m_tiles_max = m_tiles_max;
-    e = launch_moe_gemm(mode1, p.dtype, p.mfma, g1, s);
+    g1.pair_dest = pair_dest;
+    g1.fold_w = p.set_path ? 1 : 0;
+    g1.n_experts = p.E;
+    g1.seg_len = p.I;
+    {
+        ProfScope ps(kSlotGemm1, s);
+        e = launch_moe_gemm(mode1, p.dtype, p.mfma, g1, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "fused_moe gate/up GEMM");
 
-    e = launch_fill_zero_f32(acc, (long long)p.T * p.H, s);
+    if (p.set_path) {
+        // down / fc2 over the expert sets, straight into the caller's output
+        GemmArgs g2 = g1;
+        g2.A = inter;
+        g2.B0 = qwen3 ? down : up;
+        g2.B1 = nullptr;
+        g2.C = out;
+        g2.strideB = (long long)p.I * p.H;
+        g2.ldb = qwen3 ? p.H : p.I;
+        g2.K = p.k * p.I;
+        g2.N = p.H;
+        g2.offsets = tb.offsets;
+        g2.tile_row = tb.tile_row;
+        g2.tile_exp = tb.tile_exp;
+        g2.num_tiles = tb.num_tiles;
+        g2.tok_sorted = tb.sorted_pair;
+        g2.pair_dest = nullptr;
+        g2.fold_w = 0;
+        const int mode2 = qwen3 ? kDownSet : kFc2Set;
+        g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.mfma));
+        g2.m_tiles_max = (int)set_tiles_max(p);
+        {
+            ProfScope ps(kSlotGemm2, s);
+            e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+        }
+        if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM (expert sets)");
+        return CANDLE_MOE_OK;
+    }
+
+    {
+        ProfScope ps(kSlotZero, s);
+        e = launch_fill_zero_f32(acc, (long long)p.T * p.H, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "fused_moe accumulator clear");
 
     GemmArgs g2 = g1;
@@ -167,10 +311,16 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.N = p.H;
     const int mode2 = qwen3 ? kDown : kFc2;
     g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.mfma));
-    e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+    {
+        ProfScope ps(kSlotGemm2, s);
+        e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM");
 
-    e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, s);
+    {
+        ProfScope ps(kSlotFinal, s);
+        e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "fused_moe finalize");
     return CANDLE_MOE_OK;
 }
@@ -303,6 +453,56 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
 }
 
 const char* candle_moe_last_error(void) { return cm::g_last_error.c_str(); }
+
+int candle_moe_set_combine_policy(int policy) {
+    if (policy < 0 || policy > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "combine policy must be 0, 1 or 2");
+    cm::g_combine_policy = policy;
+    return CANDLE_MOE_OK;
+}
+
+int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                              int num_selected_experts, uint32_t dtype) {
+    cm::Problem p;
+    if (cm::check_problem(num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts, 0, 0, dtype, p))
+        return -1;
+    return p.set_path ? 2 : (p.mfma ? 1 : 0);
+}
+
+int candle_moe_profile_begin(void) {
+    std::lock_guard<std::mutex> lk(cm::g_prof_mu);
+    cm::g_prof_on = true;
+    return cm::kNumSlots;
+}
+
+int candle_moe_profile_end(double* total_ms, int* counts, int nslots) {
+    std::vector<cm::ProfRec> recs;
+    {
+        std::lock_guard<std::mutex> lk(cm::g_prof_mu);
+        cm::g_prof_on = false;
+        recs.swap(cm::g_prof);
+    }
+    for (int i = 0; i < nslots; ++i) {
+        if (total_ms) total_ms[i] = 0.0;
+        if (counts) counts[i] = 0;
+    }
+    int rc = CANDLE_MOE_OK;
+    for (auto& r : recs) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess)
+            rc = CANDLE_MOE_ERR_HIP;
+        else if (r.slot < nslots) {
+            if (total_ms) total_ms[r.slot] += ms;
+            if (counts) counts[r.slot] += 1;
+        }
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    return rc;
+}
+
+const char* candle_moe_profile_slot_name(int slot) {
+    return (slot >= 0 && slot < cm::kNumSlots) ? cm::kSlotNames[slot] : "";
+}
 
 const char* candle_moe_version(void) { return "candle-moe-hip 0.1.0 (gfx950)"; }
 

@@ -29,12 +29,23 @@ inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM
 hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
                            hipStream_t stream);
 
+// Tokens grouped by their expert set: the key of token t is its k expert
+// ids sorted ascending (ids >= E become E and sort last), read as base-(E+1)
+// digits. b.sorted_pair receives the token of each sorted position,
+// pair_dest[t*k + j] = pos(t)*k + rank of slot j in the token's sorted set.
+constexpr int kSetMaxK = 8;
+constexpr int kSetMaxKeys = 1024;
+hipError_t launch_token_grouping(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
+                                 int32_t* pair_dest, hipStream_t stream);
+
 // ----------------------------------------------------------- grouped GEMM
 enum GemmMode : int {
-    kGateUp = 0,  // Qwen3: inter = act(x.G) * (x.U)      (A gathered from x, B [K,N] x2)
-    kFc1 = 1,     // Nomic: inter = act(x.G)              (A gathered from x, B [K,N])
-    kDown = 2,    // Qwen3: acc[t] += w * (inter.D)       (A = inter rows, B [K,N])
-    kFc2 = 3,     // Nomic: acc[t] += w * (inter.U^T)     (A = inter rows, B [N,K])
+    kGateUp = 0,   // Qwen3: inter = act(x.G) * (x.U)      (A gathered from x, B [K,N] x2)
+    kFc1 = 1,      // Nomic: inter = act(x.G)              (A gathered from x, B [K,N])
+    kDown = 2,     // Qwen3: acc[t] += w * (inter.D)       (A = inter rows, B [K,N], f32 atomics)
+    kFc2 = 3,      // Nomic: acc[t] += w * (inter.U^T)     (A = inter rows, B [N,K], f32 atomics)
+    kDownSet = 4,  // Qwen3, tokens grouped by expert set: out[t] += [w*h_1 .. w*h_k] . [D_e1; ..; D_ek]
+    kFc2Set = 5,   // Nomic, same with the U_e^T blocks
 };
 
 struct GemmArgs {
@@ -56,6 +67,12 @@ struct GemmArgs {
     int act;                  // activation code
     int n_tiles;              // output column tiles
     int m_tiles_max;          // upper bound on row tiles (grid sizing)
+    // expert-set path
+    const int32_t* pair_dest; // GEMM1: output row of pair p (NULL: its sorted row)
+    const int32_t* tok_sorted;// set GEMM2: token of each sorted row
+    int fold_w;               // GEMM1: scale by the routing weight before rounding
+    int n_experts;            // E (key digits are base E+1)
+    int seg_len;              // set GEMM2: K length of one slot's segment (= I)
 };
 
 // Row tile used by the grouping tile table for the MFMA GEMMs.

@@ -15,6 +15,8 @@
 //                        per-block bases, expert offsets and the tile table
 //   3. grouping_scatter: each workgroup re-reads its chunk and ranks pairs
 //                        stably with wave ballots (64-lane peer masks)
+// The same three kernels group tokens by their expert set (TOK = true) for
+// the expert-set down projection.
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
 
@@ -22,22 +24,64 @@ namespace cm {
 
 constexpr int kGroupThreads = 256;
 
+// Token t's expert set: its k ids with ids >= E replaced by E, sorted
+// ascending (stable in j); the key reads them as base-(E+1) digits, most
+// significant first. rank[j] is slot j's position in that order.
+__device__ __forceinline__ int token_set_key(const uint32_t* __restrict__ idx, long long t, int k, int E,
+                                             int (&rank)[kSetMaxK]) {
+    int ex[kSetMaxK];
+    for (int j = 0; j < k; ++j) {
+        const uint32_t v = idx[t * k + j];
+        ex[j] = v < (uint32_t)E ? (int)v : E;
+    }
+    int key = 0;
+    for (int j = 0; j < k; ++j) {
+        int r = 0;
+        for (int i = 0; i < k; ++i) r += (ex[i] < ex[j]) || (ex[i] == ex[j] && i < j);
+        rank[j] = r;
+    }
+    // digits in sorted order: position r holds the slot with rank r
+    for (int r = 0; r < k; ++r) {
+        int d = E;
+        for (int j = 0; j < k; ++j) d = (rank[j] == r) ? ex[j] : d;
+        key = key * (E + 1) + d;
+    }
+    return key;
+}
+
+// Bin of item i: the expert of pair i (TOK = false, -1 if dropped), or the
+// expert-set key of token i (TOK = true).
+template <bool TOK>
+__device__ __forceinline__ int item_bin(const uint32_t* __restrict__ idx, long long i, int k, int E,
+                                        int (&rank)[kSetMaxK]) {
+    if constexpr (TOK) {
+        return token_set_key(idx, i, k, E, rank);
+    } else {
+        const uint32_t e = __builtin_nontemporal_load(idx + i);
+        return e < (uint32_t)E ? (int)e : -1;
+    }
+}
+
+template <bool TOK>
 __global__ __launch_bounds__(kGroupThreads) void grouping_hist(const uint32_t* __restrict__ idx, long long P,
-                                                               int E, int32_t* __restrict__ block_counts) {
-    extern __shared__ int32_t s_cnt[];  // [4 waves][E]
+                                                               int k, int E, int nbins,
+                                                               int32_t* __restrict__ block_counts) {
+    extern __shared__ int32_t s_cnt[];  // [4 waves][nbins]
     const int wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < 4 * E; i += kGroupThreads) s_cnt[i] = 0;
+    for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
     __syncthreads();
     const long long base = (long long)blockIdx.x * kGroupChunk;
     const long long end = base + kGroupChunk < P ? base + kGroupChunk : P;
-    int32_t* mine = s_cnt + wave * E;
+    int32_t* mine = s_cnt + wave * nbins;
+    int rank[kSetMaxK];
     for (long long p = base + threadIdx.x; p < end; p += kGroupThreads) {
-        const uint32_t e = __builtin_nontemporal_load(idx + p);
-        if (e < (uint32_t)E) atomicAdd(mine + e, 1);
+        const int b = item_bin<TOK>(idx, p, k, E, rank);
+        if (b >= 0) atomicAdd(mine + b, 1);
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += kGroupThreads)
-        block_counts[(long long)blockIdx.x * E + e] = s_cnt[e] + s_cnt[E + e] + s_cnt[2 * E + e] + s_cnt[3 * E + e];
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads)
+        block_counts[(long long)blockIdx.x * nbins + e] =
+            s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
 }
 
 // One workgroup. block_counts[b][e] becomes the number of expert-e pairs in
@@ -88,19 +132,22 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int 
     }
 }
 
+template <bool TOK>
 __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t* __restrict__ idx, long long P,
-                                                                  int E, int ebits,
+                                                                  int k, int E, int nbins, int ebits,
                                                                   const int32_t* __restrict__ block_counts,
                                                                   const int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ sorted_pair) {
+                                                                  int32_t* __restrict__ sorted_pair,
+                                                                  int32_t* __restrict__ pair_dest) {
     extern __shared__ int32_t s_mem[];
-    int32_t* s_run = s_mem;           // [E] next free position per expert
-    int32_t* s_wc = s_mem + E;        // [4][E] per-wave counts of the current step
+    const int E_ = nbins;
+    int32_t* s_run = s_mem;           // [bins] next free position per bin
+    int32_t* s_wc = s_mem + E_;       // [4][bins] per-wave counts of the current step
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    for (int e = threadIdx.x; e < E; e += kGroupThreads) {
-        s_run[e] = offsets[e] + block_counts[(long long)blockIdx.x * E + e];
-        s_wc[e] = s_wc[E + e] = s_wc[2 * E + e] = s_wc[3 * E + e] = 0;
+    for (int e = threadIdx.x; e < E_; e += kGroupThreads) {
+        s_run[e] = offsets[e] + block_counts[(long long)blockIdx.x * E_ + e];
+        s_wc[e] = s_wc[E_ + e] = s_wc[2 * E_ + e] = s_wc[3 * E_ + e] = 0;
     }
     __syncthreads();
     const long long base = (long long)blockIdx.x * kGroupChunk;
@@ -108,8 +155,10 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (long long s = base; s < end; s += kGroupThreads) {
         const long long p = s + threadIdx.x;
-        const uint32_t e = p < end ? idx[p] : 0xffffffffu;
-        const bool active = e < (uint32_t)E;
+        int rank[kSetMaxK];
+        const int bin = p < end ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        const bool active = bin >= 0;
+        const uint32_t e = active ? (uint32_t)bin : 0xffffffffu;
         // Lanes of this wave holding the same expert: AND of per-bit ballots.
         uint64_t peers = __ballot(active);
         for (int b = 0; b < ebits; ++b) {
@@ -117,39 +166,55 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t
             const uint64_t bal = __ballot(bit);
             peers &= bit ? bal : ~bal;
         }
-        const int rank = __popcll(peers & lt_mask);
-        if (active && rank == 0) s_wc[wave * E + e] = __popcll(peers);
+        const int lrank = __popcll(peers & lt_mask);
+        if (active && lrank == 0) s_wc[wave * E_ + e] = __popcll(peers);
         __syncthreads();
         if (active) {
-            int32_t pos = s_run[e] + rank;
-            for (int w = 0; w < wave; ++w) pos += s_wc[w * E + e];
+            int32_t pos = s_run[e] + lrank;
+            for (int w = 0; w < wave; ++w) pos += s_wc[w * E_ + e];
             sorted_pair[pos] = (int32_t)p;
+            if constexpr (TOK) {
+                for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
+            }
         }
         __syncthreads();
-        for (int ee = threadIdx.x; ee < E; ee += kGroupThreads) {
-            s_run[ee] += s_wc[ee] + s_wc[E + ee] + s_wc[2 * E + ee] + s_wc[3 * E + ee];
-            s_wc[ee] = s_wc[E + ee] = s_wc[2 * E + ee] = s_wc[3 * E + ee] = 0;
+        for (int ee = threadIdx.x; ee < E_; ee += kGroupThreads) {
+            s_run[ee] += s_wc[ee] + s_wc[E_ + ee] + s_wc[2 * E_ + ee] + s_wc[3 * E_ + ee];
+            s_wc[ee] = s_wc[E_ + ee] = s_wc[2 * E_ + ee] = s_wc[3 * E_ + ee] = 0;
         }
         __syncthreads();
     }
 }
 
-hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
-                           hipStream_t stream) {
-    const int nb = grouping_blocks(P);
-    int ebits = 0;
-    while ((1 << ebits) < E) ++ebits;
+template <bool TOK>
+static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int E, int nbins, int BM,
+                                const GroupingBufs& b, int32_t* pair_dest, hipStream_t stream) {
+    const int nb = grouping_blocks(items);
+    int bbits = 0;
+    while ((1 << bbits) < nbins) ++bbits;
     if (nb > 0) {
-        hipLaunchKernelGGL(grouping_hist, dim3(nb), dim3(kGroupThreads), 4 * E * sizeof(int32_t), stream, idx, P,
-                           E, b.block_counts);
+        hipLaunchKernelGGL((grouping_hist<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t), stream,
+                           idx, items, k, E, nbins, b.block_counts);
     }
-    hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), 2 * E * sizeof(int32_t), stream, nb, E, BM,
-                       b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles);
+    hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), 2 * nbins * sizeof(int32_t), stream, nb, nbins,
+                       BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles);
     if (nb > 0) {
-        hipLaunchKernelGGL(grouping_scatter, dim3(nb), dim3(kGroupThreads), 5 * E * sizeof(int32_t), stream, idx, P,
-                           E, ebits, b.block_counts, b.offsets, b.sorted_pair);
+        hipLaunchKernelGGL((grouping_scatter<TOK>), dim3(nb), dim3(kGroupThreads), 5 * nbins * sizeof(int32_t),
+                           stream, idx, items, k, E, nbins, bbits, b.block_counts, b.offsets, b.sorted_pair,
+                           pair_dest);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
+                           hipStream_t stream) {
+    return grouping_impl<false>(idx, P, 1, E, E, BM, b, nullptr, stream);
+}
+
+hipError_t launch_token_grouping(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
+                                 int32_t* pair_dest, hipStream_t stream) {
+    if (k < 1 || k > kSetMaxK || nkeys > kSetMaxKeys) return hipErrorInvalidValue;
+    return grouping_impl<true>(idx, T, k, E, nkeys, BM, b, pair_dest, stream);
 }
 
 }  // namespace cm

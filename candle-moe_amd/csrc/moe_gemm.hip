@@ -9,6 +9,12 @@
 //   kFc2     Nomic fc2     : acc[t]  += w_p * (inter[r] . U_e^T)
 // where r runs over expert-sorted pairs p = t*k + j of expert e and acc is
 // an f32 [T,N] accumulator that a final pass adds to the caller's output.
+// Expert-set path (few distinct expert sets, e.g. E=8, k=2): tokens are
+// grouped by the sorted set of their k experts, GEMM1 writes w_p * h for
+// pair p into slot rank(j) of its token's row of inter [T, k*I], and
+//   kDownSet / kFc2Set : out[t] += [w h_1 | .. | w h_k] . [B_e1; ..; B_ek]
+// one GEMM over K = k*I whose weight block switches expert every I rows, so
+// each output row is written exactly once: no atomics, no f32 accumulator.
 //
 // moe_mfma_gemm (bf16 / f16): 256 threads = 4 waves in a 2x2 layout, block
 // tile BM x BN, K staged 64 at a time through a 2-stage LDS ring.
@@ -19,9 +25,10 @@
 //  * LDS rows are 128 B with an XOR swizzle of the 16-byte chunk index by
 //    row bits [2:0] and [5:3], so fragment reads and transposed writes hit
 //    distinct banks.
-//  * v_mfma_f32_32x32x16_{bf16,f16} with the weight fragment as the MFMA A
-//    operand: each lane then owns 4 consecutive output columns of one row,
-//    which the epilogue writes as one 8-byte store (or 4 f32 atomics).
+//  * v_mfma_f32_32x32x16_{bf16,f16}. For stores the weight fragment is the
+//    MFMA A operand, so each lane owns 4 consecutive output columns of one
+//    row (one 8-byte store); for the f32 atomics the operands stay in order,
+//    so a register of the wave spans 32 consecutive columns (coalesced).
 //  * gate and up column blocks are interleaved every 32 columns, so the
 //    SwiGLU product is formed in registers.
 //  * Workgroup ids are remapped so each XCD walks a contiguous range of
@@ -56,28 +63,54 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
     constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 32, NB = WN / 32;
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
-    constexpr bool BNK = (MODE == kFc2);
+    constexpr bool SET = (MODE == kDownSet || MODE == kFc2Set);
+    constexpr bool BNK = (MODE == kFc2 || MODE == kFc2Set);
+    constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
+    // ATOMIC epilogues keep the MFMA operands unswapped, so one register of a
+    // wave covers 32 consecutive output columns of 2 rows (coalesced atomics);
+    // the others swap them, so a lane owns 4 consecutive columns of one row.
+    constexpr bool SWAP = !ATOMIC;
     constexpr int A_ITEMS = BM * 8 / 256;
     constexpr int B_ITEMS = BNK ? (BN * 8 / 256) : ((BN + 255) / 256);  // 16-B chunks or 8x8 blocks
     constexpr int B_REGS = BNK ? B_ITEMS : B_ITEMS * 8;
     constexpr int STAGE = (BM + BN) * 128;
     static_assert(!DUAL || (WN % 64) == 0, "gate/up pairs must stay inside one wave");
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    __shared__ int32_t s_tok[ATOMIC ? BM : 1];
+    __shared__ float s_w[ATOMIC ? BM : 1];
 
     int mt, nt;
     tile_coords(a.n_tiles, mt, nt);
     if (mt >= *a.num_tiles) return;
     const int r0 = a.tile_row[mt];
-    const int e = a.tile_exp[mt];
-    const int seg_end = a.offsets[e + 1];
-    const int m_valid = min(BM, seg_end - r0);
+    const int grp = a.tile_exp[mt];  // expert, or expert-set key
+    const int m_valid = min(BM, a.offsets[grp + 1] - r0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int K = a.K, N = a.N;
+    const int N = a.N;
+
+    // Experts feeding this tile: one, or the k digits of the set key (ascending;
+    // digit E marks a dropped slot and sorts last, so only the first n_seg count).
+    int seg_exp[SET ? kSetMaxK : 1];
+    int n_seg = 1;
+    if constexpr (SET) {
+        const int base = a.n_experts + 1;
+        int key = grp;
+        n_seg = 0;
+        for (int s = a.k_top - 1; s >= 0; --s) {
+            seg_exp[s] = key % base;
+            key /= base;
+        }
+        for (int s = 0; s < a.k_top; ++s) n_seg += seg_exp[s] < a.n_experts;
+    } else {
+        seg_exp[0] = grp;
+    }
+    const int K = SET ? n_seg * a.seg_len : a.K;          // reduction length of this tile
+    const int a_pitch = SET ? a.k_top * a.seg_len : a.K;  // A row pitch
 
     const uint16_t* Ab = reinterpret_cast<const uint16_t*>(a.A);
-    const uint16_t* B0 = reinterpret_cast<const uint16_t*>(a.B0) + (long long)e * a.strideB;
-    const uint16_t* B1 = DUAL ? reinterpret_cast<const uint16_t*>(a.B1) + (long long)e * a.strideB : nullptr;
+    const uint16_t* B0 = reinterpret_cast<const uint16_t*>(a.B0);
+    const uint16_t* B1 = reinterpret_cast<const uint16_t*>(a.B1);
 
     // A: thread owns chunk (tid & 7) of rows (tid >> 3) + 32 i.
     const int a_c = tid & 7;
@@ -88,39 +121,45 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
         const int rr = r < m_valid ? r : 0;
         if constexpr (GATHER) {
             const int tok = a.sorted_pair[r0 + rr] / a.k_top;
-            a_off[i] = (long long)tok * K;
+            a_off[i] = (long long)tok * a_pitch;
         } else {
-            a_off[i] = (long long)(r0 + rr) * K;
+            a_off[i] = (long long)(r0 + rr) * a_pitch;
         }
     }
-    // B source pointers and validity.
-    const uint16_t* b_ptr[B_ITEMS];
-    bool b_ok[B_ITEMS];
+    if constexpr (ATOMIC) {
+        if (tid < BM) {
+            const int p = a.sorted_pair[r0 + (tid < m_valid ? tid : 0)];
+            s_tok[tid] = p / a.k_top;
+            s_w[tid] = a.routing_w[p];
+        }
+    }
+    // B: element offsets inside one expert's matrix (k offset added per stage).
+    long long b_off[B_ITEMS];
+    bool b_ok[B_ITEMS], b_up[B_ITEMS];
     int b_kb[B_ITEMS], b_q[B_ITEMS];
 #pragma unroll
     for (int i = 0; i < B_ITEMS; ++i) {
         const int item = tid + 256 * i;
+        b_up[i] = false;
         if constexpr (BNK) {
             const int row = item >> 3, c = item & 7;
             const int col = nt * BN + row;
             b_ok[i] = col < N;
-            b_ptr[i] = B0 + (long long)(b_ok[i] ? col : 0) * a.ldb + c * 8;
+            b_off[i] = (long long)(b_ok[i] ? col : 0) * a.ldb + c * 8;
             b_kb[i] = c;
             b_q[i] = row;
         } else {
             const int q = item % (BN / 8), kb = item / (BN / 8);
             const int nr = q * 8;
             int col;
-            const uint16_t* base;
             if constexpr (DUAL) {
                 col = nt * (BN / 2) + (nr >> 6) * 32 + (nr & 31);
-                base = ((nr >> 5) & 1) ? B1 : B0;
+                b_up[i] = ((nr >> 5) & 1) != 0;
             } else {
                 col = nt * BN + nr;
-                base = B0;
             }
             b_ok[i] = (item < BN) && (col < N);
-            b_ptr[i] = base + (long long)kb * 8 * a.ldb + (b_ok[i] ? col : 0);
+            b_off[i] = (long long)kb * 8 * a.ldb + (b_ok[i] ? col : 0);
             b_kb[i] = kb;
             b_q[i] = q;
         }
@@ -144,16 +183,26 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
             const bool ok = (k0 + a_c * 8) < K;
             ra[i] = ok ? *reinterpret_cast<const u32x4*>(Ab + a_off[i] + k0 + a_c * 8) : zero4;
         }
+        // expert matrix and K offset inside it for this stage
+        int kk = k0, klim = K, e = seg_exp[0];
+        if constexpr (SET) {
+            const int s = k0 / a.seg_len;
+            e = seg_exp[s < kSetMaxK ? s : 0];
+            kk = k0 - s * a.seg_len;
+            klim = a.seg_len;
+        }
+        const uint16_t* g0 = B0 + (long long)e * a.strideB;
+        const uint16_t* g1 = DUAL ? B1 + (long long)e * a.strideB : g0;
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
+            const bool ok = b_ok[i] && (k0 < K) && (kk + b_kb[i] * 8) < klim;
             if constexpr (BNK) {
-                const bool ok = b_ok[i] && (k0 + b_kb[i] * 8) < K;
-                rb[i] = ok ? *reinterpret_cast<const u32x4*>(b_ptr[i] + k0) : zero4;
+                rb[i] = ok ? *reinterpret_cast<const u32x4*>(g0 + b_off[i] + kk) : zero4;
             } else {
-                const bool ok = b_ok[i] && (k0 + b_kb[i] * 8) < K;
+                const uint16_t* src = (b_up[i] ? g1 : g0) + b_off[i] + (long long)kk * a.ldb;
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    rb[i * 8 + j] = ok ? *reinterpret_cast<const u32x4*>(b_ptr[i] + (long long)(k0 + j) * a.ldb) : zero4;
+                    rb[i * 8 + j] = ok ? *reinterpret_cast<const u32x4*>(src + (long long)j * a.ldb) : zero4;
             }
         }
     };
@@ -204,13 +253,18 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<DT>(bf[nb], af[mb], acc[mb][nb]);
+                for (int nb = 0; nb < NB; ++nb) {
+                    if constexpr (SWAP) acc[mb][nb] = mfma32<DT>(bf[nb], af[mb], acc[mb][nb]);
+                    else acc[mb][nb] = mfma32<DT>(af[mb], bf[nb], acc[mb][nb]);
+                }
         }
     };
 
     const int nk = (K + kBK - 1) / kBK;
-    load_tiles(0);
-    store_tiles(0);
+    if (nk > 0) {
+        load_tiles(0);
+        store_tiles(0);
+    }
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
@@ -220,52 +274,84 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
         __syncthreads();
     }
 
-    // ---------------- epilogue: lane owns row (lane & 31), 4 consecutive columns
-    const int nsub = 4 * (lane >> 5);
+    // ------------------------------------------------------------ epilogue
+    if constexpr (ATOMIC) {
+        // lane owns column (lane & 31) of rows 8*(i/4) + 4*(lane/32) + i%4
+        float* C = reinterpret_cast<float*>(a.C);
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int ml = wm * WM + mb * 32 + (lane & 31);
-        if (ml >= m_valid) continue;
-        const int r = r0 + ml;
-        if constexpr (MODE == kGateUp || MODE == kFc1) {
-            uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)r * N;
-            constexpr int PAIRS = DUAL ? NB / 2 : NB;
+        for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-            for (int q = 0; q < PAIRS; ++q) {
-                const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
+            for (int i = 0; i < 16; ++i) {
+                const int ml = wm * WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                if (ml >= m_valid) continue;
+                const long long rowoff = (long long)s_tok[ml] * N;
+                const float w = s_w[ml];
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int col = colbase + 8 * g + nsub;
-                    if (col >= N) continue;
-                    float h[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if constexpr (DUAL) {
-                            h[j] = act_f32(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
-                        } else {
-                            h[j] = act_f32(acc[mb][q][4 * g + j], a.act);
-                        }
-                    }
-                    u32x2 v;
-                    v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
-                    v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
-                    *reinterpret_cast<u32x2*>(C + col) = v;
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int col = nt * BN + wn * WN + nb * 32 + (lane & 31);
+                    if (col < N) unsafeAtomicAdd(C + rowoff + col, w * acc[mb][nb][i]);
                 }
             }
-        } else {
-            const int p = a.sorted_pair[r];
-            const int tok = p / a.k_top;
-            const float w = a.routing_w[p];
-            float* C = reinterpret_cast<float*>(a.C) + (long long)tok * N;
+        }
+    } else {
+        // lane owns row (lane & 31) and 4 consecutive columns per register group
+        const int nsub = 4 * (lane >> 5);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const int colbase = nt * BN + wn * WN + nb * 32;
+        for (int mb = 0; mb < MB; ++mb) {
+            const int ml = wm * WM + mb * 32 + (lane & 31);
+            if (ml >= m_valid) continue;
+            const int r = r0 + ml;
+            if constexpr (MODE == kGateUp || MODE == kFc1) {
+                const int p = a.sorted_pair[r];
+                const int dst = a.pair_dest ? a.pair_dest[p] : r;
+                const float wscale = a.fold_w ? a.routing_w[p] : 1.0f;
+                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)dst * N;
+                constexpr int PAIRS = DUAL ? NB / 2 : NB;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int col = colbase + 8 * g + nsub;
-                    if (col >= N) continue;
+                for (int q = 0; q < PAIRS; ++q) {
+                    const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) unsafeAtomicAdd(C + col + j, w * acc[mb][nb][4 * g + j]);
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = colbase + 8 * g + nsub;
+                        if (col >= N) continue;
+                        float h[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            if constexpr (DUAL) {
+                                h[j] = act_f32(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
+                            } else {
+                                h[j] = act_f32(acc[mb][q][4 * g + j], a.act);
+                            }
+                            h[j] *= wscale;
+                        }
+                        u32x2 v;
+                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
+                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                        *reinterpret_cast<u32x2*>(C + col) = v;
+                    }
+                }
+            } else {
+                // expert-set down projection: each token's row is written once
+                const int tok = a.tok_sorted[r];
+                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)tok * N;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int colbase = nt * BN + wn * WN + nb * 32;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = colbase + 8 * g + nsub;
+                        if (col >= N) continue;
+                        const u32x2 old = *reinterpret_cast<const u32x2*>(C + col);
+                        float h[4];
+                        h[0] = Elem<DT>::to_f32((uint16_t)(old[0] & 0xffffu)) + acc[mb][nb][4 * g + 0];
+                        h[1] = Elem<DT>::to_f32((uint16_t)(old[0] >> 16)) + acc[mb][nb][4 * g + 1];
+                        h[2] = Elem<DT>::to_f32((uint16_t)(old[1] & 0xffffu)) + acc[mb][nb][4 * g + 2];
+                        h[3] = Elem<DT>::to_f32((uint16_t)(old[1] >> 16)) + acc[mb][nb][4 * g + 3];
+                        u32x2 v;
+                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
+                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                        *reinterpret_cast<u32x2*>(C + col) = v;
+                    }
                 }
             }
         }
@@ -458,9 +544,13 @@ static hipError_t launch_mode(bool use_mfma, const GemmArgs& a, hipStream_t stre
             hipLaunchKernelGGL((moe_mfma_gemm<DT, BM, BN, MODE>), dim3(nwg), dim3(256), 0, stream, a);
         }
     } else {
-        const int nwg = a.m_tiles_max * a.n_tiles;
-        if (nwg <= 0) return hipSuccess;
-        hipLaunchKernelGGL((moe_simt_gemm<DT, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+        if constexpr (MODE == kDownSet || MODE == kFc2Set) {
+            return hipErrorInvalidValue;  // the expert-set path is MFMA-only
+        } else {
+            const int nwg = a.m_tiles_max * a.n_tiles;
+            if (nwg <= 0) return hipSuccess;
+            hipLaunchKernelGGL((moe_simt_gemm<DT, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+        }
     }
     return hipGetLastError();
 }
@@ -472,6 +562,8 @@ static hipError_t launch_dt(int mode, bool use_mfma, const GemmArgs& a, hipStrea
         case kFc1: return launch_mode<DT, kFc1>(use_mfma, a, stream);
         case kDown: return launch_mode<DT, kDown>(use_mfma, a, stream);
         case kFc2: return launch_mode<DT, kFc2>(use_mfma, a, stream);
+        case kDownSet: return launch_mode<DT, kDownSet>(use_mfma, a, stream);
+        case kFc2Set: return launch_mode<DT, kFc2Set>(use_mfma, a, stream);
         default: return hipErrorInvalidValue;
     }
 }

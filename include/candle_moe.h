@@ -111,6 +111,24 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
                             int num_selected_experts, int activation_type, uint32_t moe_type,
                             uint32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Per-kernel timing for benchmarks: between begin and end, every internal
+ * launch is bracketed by HIP events on the caller's stream. end() waits for
+ * those events and returns, per slot, the summed milliseconds and the number
+ * of launches; begin() returns the number of slots. */
+int candle_moe_profile_begin(void);
+int candle_moe_profile_end(double* total_ms, int* counts, int nslots);
+const char* candle_moe_profile_slot_name(int slot);
+
+/* Combine strategy of fused_moe (process-wide): 0 = choose per call (default),
+ * 1 = always the pair path (f32 accumulator + atomic scatter-add),
+ * 2 = the expert-set path whenever the shape allows it (MFMA dtypes,
+ *     intermediate_dim % 64 == 0, (E+1)^k <= 1024, k <= 8). */
+int candle_moe_set_combine_policy(int policy);
+/* Which path fused_moe takes for these sizes under the current policy:
+ * 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path, -1 invalid. */
+int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                              int num_selected_experts, uint32_t dtype);
+
 /* Message of the last failing call on this host thread ("" if none). */
 const char* candle_moe_last_error(void);
 const char* candle_moe_version(void);

@@ -185,8 +185,13 @@ def test_workspace_size():
     small = L.candle_moe_fused_moe_workspace_size(32, 64, 256, 8, 2, 1)
     big = L.candle_moe_fused_moe_workspace_size(32768, 4096, 1536, 8, 2, 1)
     assert 0 < small < big
-    # holds at least the bf16 intermediate [T*k, I] and the f32 accumulator [T, H]
-    assert big >= 65536 * 1536 * 2 + 32768 * 4096 * 4
+    # the expert-set path needs the bf16 intermediate [T*k, I] only ...
+    assert cm.fused_moe_path(32768, 4096, 1536, 8, 2, 1) == "expert-set"
+    assert 65536 * 1536 * 2 <= big < 65536 * 1536 * 2 + 32768 * 4096 * 4
+    # ... the pair path also the f32 accumulator [T, H]
+    assert cm.fused_moe_path(4096, 2048, 768, 128, 8, 1) == "pairs"
+    q30 = L.candle_moe_fused_moe_workspace_size(4096, 2048, 768, 128, 8, 1)
+    assert q30 >= 32768 * 768 * 2 + 4096 * 2048 * 4
     assert L.candle_moe_fused_moe_workspace_size(32, 64, 256, 0, 2, 1) == 0
     # workspace variant: too-small workspace is refused before anything runs
     rc = L.candle_moe_fused_moe_ws(*([ctypes.c_void_p(256)] * 7), 32, 64, 256, 8, 2, 0, 0, 1,

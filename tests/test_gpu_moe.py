@@ -194,3 +194,53 @@ def test_nomic_full_size_sampled():
 @pytest.mark.slow
 def test_qwen3_30b_prefill_sampled():
     check_case(4096, 2048, 768, 128, 8, O.BF16, O.QWEN3, seed=17, zipf=1.1, rows=[0, 1, 100, 2047, 4095])
+
+
+# ---- the two combine paths (expert-set GEMM vs pair GEMM + f32 atomics) on the same inputs
+SET_CASES = [
+    # T, H, I, E, k, dtype, moe_type, act
+    (4096, 256, 128, 8, 2, O.BF16, O.QWEN3, O.SILU),
+    (4096, 256, 192, 8, 2, O.F16, O.NOMIC, O.GELU),
+    (2048, 128, 64, 8, 1, O.BF16, O.QWEN3, O.RELU),
+    (4096, 128, 128, 8, 3, O.BF16, O.QWEN3, O.SILU),
+    (3000, 192, 128, 4, 2, O.BF16, O.NOMIC, O.SILU),
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,k,dt,mt,act", SET_CASES)
+def test_expert_set_path_matches_pair_path(T, H, I, E, k, dt, mt, act):
+    try:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_EXPERT_SETS)
+        assert candle_moe.fused_moe_path(T, H, I, E, k, dt) == "expert-set"
+        a = check_case(T, H, I, E, k, dt, mt, act=act, seed=20 + k, rows=list(range(0, T, 97)))
+        candle_moe.set_combine_policy(candle_moe.COMBINE_PAIRS)
+        assert candle_moe.fused_moe_path(T, H, I, E, k, dt) == "pairs"
+        b = check_case(T, H, I, E, k, dt, mt, act=act, seed=20 + k, rows=list(range(0, T, 97)))
+    finally:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+    assert_close(a, b, RTOL[dt], "expert-set vs pair path")
+
+
+def test_expert_set_path_dropped_and_repeated_experts():
+    # ids >= E are dropped; the raw ABI also allows a token to name one expert twice
+    T, H, I, E, k = 2048, 128, 128, 8, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 30, O.QWEN3)
+    ri = ri.copy()
+    ri[::5, 1] = 77
+    ri[1::7, 1] = ri[1::7, 0]
+    ri[2::11, :] = 9
+    try:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_EXPERT_SETS)
+        got = run_moe(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16)
+    finally:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+    kw = dict(E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16)
+    assert_close(got, O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_F32ACC, **kw), RTOL[O.BF16], "f32acc")
+    assert_close(got, O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_EXACT, **kw), RTOL[O.BF16], "exact")
+    assert (got[2::11] == 0).all()
+
+
+def test_headline_shape_takes_expert_set_path():
+    assert candle_moe.fused_moe_path(32768, 4096, 1536, 8, 2, O.BF16) == "expert-set"
+    assert candle_moe.fused_moe_path(4096, 2048, 768, 128, 8, O.BF16) == "pairs"
+    assert candle_moe.fused_moe_path(32, 64, 256, 8, 2, O.F32) == "simt"
