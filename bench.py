@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-sample", type=int, default=2048, help="tokens in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--tile", type=int, default=0, choices=range(9),
+                    help="GEMM kernel: 0 auto, 1/2 register-staged 128/256, 3/4/5 LDS-DMA 256, 256x128, 128")
+    ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
     return ap.parse_args()
 
 
@@ -70,6 +73,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L = cm.lib()
+    cm.set_tile_policy(args.tile)
+    cm.set_combine_policy(args.combine)
 
     if args.workload == "router":
         return bench_router_only(args, torch, cm, dev)

@@ -21,7 +21,9 @@ import os
 from typing import Optional, Sequence
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "libcandle_moe_hip.so")
+# CANDLE_MOE_LIB selects another build of the library (e.g. one compiled for
+# profiling); by default the in-tree libcandle_moe_hip.so is loaded.
+LIB_PATH = os.environ.get("CANDLE_MOE_LIB") or os.path.join(os.path.dirname(_HERE), "libcandle_moe_hip.so")
 
 CANDLE_MOE_OK = 0
 CANDLE_MOE_ERR_INVALID = 1
@@ -102,6 +104,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_ws.restype = i32
         L.candle_moe_set_combine_policy.argtypes = [i32]
         L.candle_moe_set_combine_policy.restype = i32
+        L.candle_moe_set_tile_policy.argtypes = [i32]
+        L.candle_moe_set_tile_policy.restype = i32
         L.candle_moe_fused_moe_path.argtypes = [i32] * 5 + [u32]
         L.candle_moe_fused_moe_path.restype = i32
         L.candle_moe_profile_begin.argtypes = []
@@ -277,13 +281,35 @@ def set_combine_policy(policy: int) -> None:
     check(lib().candle_moe_set_combine_policy(int(policy)))
 
 
+TILE_AUTO, TILE_128, TILE_256, TILE_LDS_256, TILE_LDS_256x128, TILE_LDS_128, TILE_LDS_256K64, TILE_W8, TILE_W8K32 = range(9)
+_TILE_ROWS = {0: 64, 1: 128, 2: 256, 3: 256, 4: 256, 5: 128, 6: 256, 7: 256, 8: 256}
+
+
+def set_tile_policy(policy: int) -> None:
+    """Process-wide MFMA block tile of fused_moe (TILE_*; default auto)."""
+    check(lib().candle_moe_set_tile_policy(int(policy)))
+
+
 def fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> str:
     """Name of the path fused_moe takes for these sizes under the current policy."""
-    return PATH_NAMES[lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k,
-                                                      dtype_code)]
+    code = lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
+    return PATH_NAMES[code if code < 0 else code & 3]
+
+
+def fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> int:
+    """GEMM kernel code (TILE_*) fused_moe uses for these sizes (-1 if invalid)."""
+    code = lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
+    return -1 if code < 0 else code >> 2
+
+
+def fused_moe_tile(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> int:
+    """Block-tile rows of the GEMM kernels fused_moe uses for these sizes (64 for SIMT)."""
+    k = fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
+    return 0 if k < 0 else _TILE_ROWS[k]
 
 
 __all__ = [
     "Activation", "FusedMoE", "apply_topk_softmax_inplace", "CandleMoeError", "lib", "describe", "spec",
     "validate_topk_softmax", "version", "LIB_PATH", "set_combine_policy", "fused_moe_path",
+    "set_tile_policy", "fused_moe_tile", "fused_moe_kernel",
 ]

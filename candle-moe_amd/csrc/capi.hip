@@ -106,6 +106,7 @@ int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void*
 struct Problem {
     int T, H, I, E, k, act, moe_type, dtype;
     bool mfma;
+    int cfg;  // TileCfg of both GEMMs
     int BM;
     long long P;
     bool set_path;  // expert-set down projection (no atomics, no f32 accumulator)
@@ -121,6 +122,8 @@ struct Layout {
 // 0: choose per call; 1: always the pair path (f32 atomics); 2: the
 // expert-set path whenever the shape allows it.
 static int g_combine_policy = 0;
+// 0: choose the MFMA tile per call; kTile128 / kTile256: force it.
+static int g_tile_policy = 0;
 
 static long long set_tiles_max(const Problem& p) {
     return (p.T + p.BM - 1) / p.BM + (p.nkeys < p.T ? p.nkeys : p.T);
@@ -177,7 +180,16 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.T = T; p.H = H; p.I = I; p.E = E; p.k = k; p.act = act; p.moe_type = (int)moe_type; p.dtype = (int)dtype;
     p.P = P;
     p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
-    p.BM = p.mfma ? kMfmaBM : kSimtBM;
+    // Default MFMA kernel: LDS-DMA, 256x256 block tile, 8 waves (measured
+    // fastest on every BASELINE shape, including the skewed E=128 one).
+    p.cfg = !p.mfma ? kTileSimt : (g_tile_policy ? g_tile_policy : kLds256w8);
+    // the LDS-DMA kernels address operands with 32-bit buffer offsets
+    if (is_lds_cfg(p.cfg)) {
+        const long long es = 2;
+        const long long lim = 0x7fffff00LL;
+        if ((long long)T * H * es >= lim || P * I * es >= lim || (long long)H * I * es >= lim) p.cfg = kTile128;
+    }
+    p.BM = tile_rows(p.cfg);
     // Expert-set path: each distinct sorted expert set becomes one GEMM group
     // over K = k*I; worth it when the sets are few next to the tokens (on
     // average at least half a row tile per set, e.g. E=8, k=2 from T >= 1792).
@@ -191,7 +203,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             for (int j = 0; j < k; ++j) sets = sets * (E - j) / (j + 1);
             if (sets < 1.0) sets = 1.0;
             p.nkeys = (int)nk;
-            p.set_path = g_combine_policy == 2 || (double)T >= 0.5 * kMfmaBM * sets;
+            p.set_path = g_combine_policy == 2 || (double)T >= 0.5 * p.BM * sets;
         }
     }
     return CANDLE_MOE_OK;
@@ -253,15 +265,16 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.k_top = p.k;
     g1.act = p.act;
     const int mode1 = qwen3 ? kGateUp : kFc1;
-    g1.n_tiles = cdiv(p.I, gemm_tile_cols(mode1, p.mfma));
+    g1.n_tiles = cdiv(p.I, gemm_tile_cols(mode1, p.cfg));
     g1.m_tiles_max = m_tiles_max;
+    g1.a_bytes = (long long)p.T * p.H * (p.dtype == kF32 ? 4 : 2);
     g1.pair_dest = pair_dest;
     g1.fold_w = p.set_path ? 1 : 0;
     g1.n_experts = p.E;
     g1.seg_len = p.I;
     {
         ProfScope ps(kSlotGemm1, s);
-        e = launch_moe_gemm(mode1, p.dtype, p.mfma, g1, s);
+        e = launch_moe_gemm(mode1, p.dtype, p.cfg, g1, s);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe gate/up GEMM");
 
@@ -276,6 +289,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.ldb = qwen3 ? p.H : p.I;
         g2.K = p.k * p.I;
         g2.N = p.H;
+        g2.a_bytes = p.P * p.I * 2;
         g2.offsets = tb.offsets;
         g2.tile_row = tb.tile_row;
         g2.tile_exp = tb.tile_exp;
@@ -284,11 +298,11 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.pair_dest = nullptr;
         g2.fold_w = 0;
         const int mode2 = qwen3 ? kDownSet : kFc2Set;
-        g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.mfma));
+        g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.cfg));
         g2.m_tiles_max = (int)set_tiles_max(p);
         {
             ProfScope ps(kSlotGemm2, s);
-            e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+            e = launch_moe_gemm(mode2, p.dtype, p.cfg, g2, s);
         }
         if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM (expert sets)");
         return CANDLE_MOE_OK;
@@ -309,11 +323,12 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.ldb = qwen3 ? p.H : p.I;
     g2.K = p.I;
     g2.N = p.H;
+    g2.a_bytes = p.P * p.I * (p.dtype == kF32 ? 4 : 2);
     const int mode2 = qwen3 ? kDown : kFc2;
-    g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.mfma));
+    g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.cfg));
     {
         ProfScope ps(kSlotGemm2, s);
-        e = launch_moe_gemm(mode2, p.dtype, p.mfma, g2, s);
+        e = launch_moe_gemm(mode2, p.dtype, p.cfg, g2, s);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM");
 
@@ -460,12 +475,19 @@ int candle_moe_set_combine_policy(int policy) {
     return CANDLE_MOE_OK;
 }
 
+int candle_moe_set_tile_policy(int policy) {
+    if (policy < 0 || policy >= cm::kNumTileCfgs)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "tile policy must be in [0, %d)", cm::kNumTileCfgs);
+    cm::g_tile_policy = policy;
+    return CANDLE_MOE_OK;
+}
+
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype) {
     cm::Problem p;
     if (cm::check_problem(num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts, 0, 0, dtype, p))
         return -1;
-    return p.set_path ? 2 : (p.mfma ? 1 : 0);
+    return (p.set_path ? 2 : (p.mfma ? 1 : 0)) | (p.cfg << 2);
 }
 
 int candle_moe_profile_begin(void) {

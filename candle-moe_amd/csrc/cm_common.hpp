@@ -69,6 +69,25 @@ __device__ __forceinline__ float act_f32(float x, int act) {
     return x / (1.0f + expf(-x));
 }
 
+// The same activations from the hardware base-2 exponential (v_exp_f32) and
+// reciprocal (v_rcp_f32), a few f32 ulp from act_f32: used by the 16-bit
+// MFMA epilogues, whose results are rounded to bf16 / f16 right after.
+//   silu(x) = x * 1 / (1 + 2^(-x log2 e))
+//   gelu(x) = x * 1 / (1 + 2^(-2 log2 e * sqrt(2/pi) (x + 0.044715 x^3)))
+//             (0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)))
+__device__ __forceinline__ float act_fast(float x, int act) {
+    if (act == kRelu) return fmaxf(x, 0.0f);
+    float z;
+    if (act == kGelu) {
+        const float k = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+        z = k * (x + 0.044715f * x * x * x);
+    } else {
+        z = -1.4426950408889634f * x;
+    }
+    // clamp keeps 2^z finite (the quotient is then 0 to f32 precision)
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fminf(z, 126.0f)));
+}
+
 // ---------------------------------------------------------------------
 // wave64 cross-lane exchange: lane L receives the value of lane L ^ m.
 // m = 1, 2 : DPP quad_perm; m = 4, 8, 16 : ds_swizzle bitmask mode

@@ -73,16 +73,35 @@ struct GemmArgs {
     int fold_w;               // GEMM1: scale by the routing weight before rounding
     int n_experts;            // E (key digits are base E+1)
     int seg_len;              // set GEMM2: K length of one slot's segment (= I)
+    long long a_bytes;        // size of A in bytes (LDS-DMA kernels: buffer range, < 2^31)
 };
 
-// Row tile used by the grouping tile table for the MFMA GEMMs.
-constexpr int kMfmaBM = 128;
-constexpr int kSimtBM = 64;
+// Kernel shapes. kTileSimt: 64x64 SIMT; kTile128 / kTile256: MFMA kernels
+// with 128x128 / 256x256 block tiles (the grouping tile table must be built
+// with the same row tile, tile_rows()).
+// kLds*: the LDS-DMA kernels (moe_gemm_lds.hip): 256x256 with BK=32 and 4
+// stages, 256x128 BK=64 3 stages, 128x128 BK=64 4 stages, 256x256 BK=64
+// 2 stages.
+// kLds256w8 / kLds256w8k32: 256x256 with 8 waves (2 per SIMD), BK=64 2 stages
+// / BK=32 4 stages.
+enum TileCfg : int {
+    kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
+    kLds256w8 = 7, kLds256w8k32 = 8
+};
+constexpr int kNumTileCfgs = 9;
+inline int tile_rows(int cfg) {
+    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128) ? 128 : 256);
+}
+inline int tile_cols(int cfg) {
+    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128) ? 128 : 256);
+}
+inline bool is_lds_cfg(int cfg) { return cfg >= kLds256; }
 
 bool mfma_supported(int dtype, int K, int N);
 // Logical output columns covered by one workgroup of the chosen kernel.
-int gemm_tile_cols(int mode, bool use_mfma);
-hipError_t launch_moe_gemm(int mode, int dtype, bool use_mfma, const GemmArgs& a, hipStream_t stream);
+int gemm_tile_cols(int mode, int cfg);
+hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
+hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);

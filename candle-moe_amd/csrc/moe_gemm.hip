@@ -59,7 +59,7 @@ __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return __b
 __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 template <int DT, int BM, int BN, int MODE>
-__global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
+__global__ __launch_bounds__(256, 1) void moe_mfma_gemm(GemmArgs a) {
     constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 32, NB = WN / 32;
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
@@ -318,9 +318,9 @@ __global__ __launch_bounds__(256) void moe_mfma_gemm(GemmArgs a) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
                             if constexpr (DUAL) {
-                                h[j] = act_f32(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
+                                h[j] = act_fast(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
                             } else {
-                                h[j] = act_f32(acc[mb][q][4 * g + j], a.act);
+                                h[j] = act_fast(acc[mb][q][4 * g + j], a.act);
                             }
                             h[j] *= wscale;
                         }
@@ -525,30 +525,28 @@ bool mfma_supported(int dtype, int K, int N) {
     return (dtype == kBF16 || dtype == kF16) && (K % 8 == 0) && (N % 8 == 0);
 }
 
-constexpr int kMfmaBN = 128;
-
-int gemm_tile_cols(int mode, bool use_mfma) {
-    if (!use_mfma) return 64;
-    return mode == kGateUp ? kMfmaBN / 2 : kMfmaBN;
+int gemm_tile_cols(int mode, int cfg) {
+    const int bn = tile_cols(cfg);
+    return (mode == kGateUp && cfg != kTileSimt) ? bn / 2 : bn;
 }
 
 template <int DT, int MODE>
-static hipError_t launch_mode(bool use_mfma, const GemmArgs& a, hipStream_t stream) {
-    if (use_mfma) {
+static hipError_t launch_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
+    const int nwg = a.m_tiles_max * a.n_tiles;
+    if (nwg <= 0) return hipSuccess;
+    if (cfg == kTile128 || cfg == kTile256) {
         if constexpr (DT == kF32) {
             return hipErrorInvalidValue;
         } else {
-            constexpr int BM = kMfmaBM, BN = kMfmaBN;
-            const int nwg = a.m_tiles_max * a.n_tiles;
-            if (nwg <= 0) return hipSuccess;
-            hipLaunchKernelGGL((moe_mfma_gemm<DT, BM, BN, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+            if (cfg == kTile256)
+                hipLaunchKernelGGL((moe_mfma_gemm<DT, 256, 256, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+            else
+                hipLaunchKernelGGL((moe_mfma_gemm<DT, 128, 128, MODE>), dim3(nwg), dim3(256), 0, stream, a);
         }
     } else {
         if constexpr (MODE == kDownSet || MODE == kFc2Set) {
             return hipErrorInvalidValue;  // the expert-set path is MFMA-only
         } else {
-            const int nwg = a.m_tiles_max * a.n_tiles;
-            if (nwg <= 0) return hipSuccess;
             hipLaunchKernelGGL((moe_simt_gemm<DT, MODE>), dim3(nwg), dim3(256), 0, stream, a);
         }
     }
@@ -556,22 +554,23 @@ static hipError_t launch_mode(bool use_mfma, const GemmArgs& a, hipStream_t stre
 }
 
 template <int DT>
-static hipError_t launch_dt(int mode, bool use_mfma, const GemmArgs& a, hipStream_t stream) {
+static hipError_t launch_dt(int mode, int cfg, const GemmArgs& a, hipStream_t stream) {
     switch (mode) {
-        case kGateUp: return launch_mode<DT, kGateUp>(use_mfma, a, stream);
-        case kFc1: return launch_mode<DT, kFc1>(use_mfma, a, stream);
-        case kDown: return launch_mode<DT, kDown>(use_mfma, a, stream);
-        case kFc2: return launch_mode<DT, kFc2>(use_mfma, a, stream);
-        case kDownSet: return launch_mode<DT, kDownSet>(use_mfma, a, stream);
-        case kFc2Set: return launch_mode<DT, kFc2Set>(use_mfma, a, stream);
+        case kGateUp: return launch_mode<DT, kGateUp>(cfg, a, stream);
+        case kFc1: return launch_mode<DT, kFc1>(cfg, a, stream);
+        case kDown: return launch_mode<DT, kDown>(cfg, a, stream);
+        case kFc2: return launch_mode<DT, kFc2>(cfg, a, stream);
+        case kDownSet: return launch_mode<DT, kDownSet>(cfg, a, stream);
+        case kFc2Set: return launch_mode<DT, kFc2Set>(cfg, a, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_moe_gemm(int mode, int dtype, bool use_mfma, const GemmArgs& a, hipStream_t stream) {
-    if (dtype == kBF16) return launch_dt<kBF16>(mode, use_mfma, a, stream);
-    if (dtype == kF16) return launch_dt<kF16>(mode, use_mfma, a, stream);
-    if (dtype == kF32) return launch_dt<kF32>(mode, use_mfma, a, stream);
+hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
+    if (is_lds_cfg(cfg)) return launch_moe_gemm_lds(mode, dtype, cfg, a, stream);
+    if (dtype == kBF16) return launch_dt<kBF16>(mode, cfg, a, stream);
+    if (dtype == kF16) return launch_dt<kF16>(mode, cfg, a, stream);
+    if (dtype == kF32) return launch_dt<kF32>(mode, cfg, a, stream);
     return hipErrorInvalidValue;
 }
 

@@ -124,8 +124,13 @@ const char* candle_moe_profile_slot_name(int slot);
  * 2 = the expert-set path whenever the shape allows it (MFMA dtypes,
  *     intermediate_dim % 64 == 0, (E+1)^k <= 1024, k <= 8). */
 int candle_moe_set_combine_policy(int policy);
-/* Which path fused_moe takes for these sizes under the current policy:
- * 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path, -1 invalid. */
+/* GEMM kernel of fused_moe (process-wide): 0 = choose per call (default);
+ * register-staged MFMA kernels 1 = 128x128, 2 = 256x256 block tiles;
+ * LDS-DMA MFMA kernels 3 = 256x256, 4 = 256x128, 5 = 128x128. */
+int candle_moe_set_tile_policy(int policy);
+/* Which path fused_moe takes for these sizes under the current policies:
+ * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
+ * bits 2-4: the GEMM kernel (policy code above); -1 = invalid sizes. */
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype);
 

@@ -244,3 +244,18 @@ def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32768, 4096, 1536, 8, 2, O.BF16) == "expert-set"
     assert candle_moe.fused_moe_path(4096, 2048, 768, 128, 8, O.BF16) == "pairs"
     assert candle_moe.fused_moe_path(32, 64, 256, 8, 2, O.F32) == "simt"
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("combine", [1, 2])
+def test_tile_configs(tile, combine):
+    # both MFMA block tiles on both combine paths, ragged groups and column tails
+    try:
+        candle_moe.set_tile_policy(tile)
+        candle_moe.set_combine_policy(combine)
+        check_case(3000, 320, 200, 8, 2, O.BF16, O.QWEN3, seed=40 + tile, rows=list(range(0, 3000, 37)))
+        check_case(2500, 264, 448, 6, 2, O.F16, O.NOMIC, act=O.GELU, seed=41 + tile, rows=list(range(0, 2500, 41)))
+        check_case(700, 128, 64, 8, 1, O.BF16, O.QWEN3, seed=42 + tile)
+    finally:
+        candle_moe.set_tile_policy(0)
+        candle_moe.set_combine_policy(0)
