@@ -51,11 +51,28 @@ def parse():
     ap.add_argument("--tokens", type=int, default=0, help="override T")
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-sample", type=int, default=2048, help="tokens in the CPU-baseline sample (0 = skip)")
-    ap.add_argument("--tile", type=int, default=0, choices=range(9),
-                    help="GEMM kernel: 0 auto, 1/2 register-staged 128/256, 3/4/5 LDS-DMA 256, 256x128, 128")
+    ap.add_argument("--cpu-sample", type=int, default=32768,
+                    help="tokens in the CPU-baseline sample (0 = skip; default: the whole batch)")
+    ap.add_argument("--tile", type=int, default=0, choices=range(12),
+                    help="GEMM kernel: 0 auto, 1/2 register-staged 128/256, 3-8, 10, 11 LDS-DMA variants, 9 ping-pong")
     ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="before the warmup, run 3 plain copy kernels of MIB MiB (read MIB, write MIB; "
+                         "the reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_calibration(torch, dev, mib):
+    """A plain streaming kernel of known traffic: b = -a over `mib` MiB of f32
+    (reads exactly mib MiB, writes exactly mib MiB)."""
+    n = (mib << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def main():
@@ -106,6 +123,8 @@ def main():
     tok_ei = torch.empty((T, k), dtype=torch.int32, device=dev)
     moe = cm.FusedMoE.new(E, k, act)
     torch.cuda.synchronize()
+    if args.copy_calibration:
+        copy_calibration(torch, dev, args.copy_calibration)
 
     def step():
         cm.apply_topk_softmax_inplace(logits, topk_w, topk_i, tok_ei)
@@ -142,7 +161,7 @@ def main():
     g1_achieved = g1_flops / (g1_us * 1e-6) / 1e12 if g1_us else 0.0
     topk_us = kernels.get("topk_softmax", 0.0)
     topk_bytes = T * E * 4 + T * k * 12
-    traffic = load_traffic(args.workload, wl)
+    traffic = load_traffic(args.workload, wl, args.tile)
 
     cpu = None
     if args.cpu_sample > 0:
@@ -187,15 +206,17 @@ def main():
     del out
 
 
-def load_traffic(workload, wl):
+def load_traffic(workload, wl, tile):
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 --pmc summary (profiles/traffic.json), or None."""
+    rocprofv3 --pmc measurement (profiles/traffic.json: FETCH_SIZE and
+    WRITE_SIZE scaled by a plain 1 GiB copy), or None when the workload,
+    token count or GEMM kernel differs from the measured one."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
         rec = d.get(workload)
-        if rec and rec.get("tokens") == wl["T"]:
+        if rec and rec.get("tokens") == wl["T"] and wl["dtype"] == "bf16" and tile == 0:
             return rec.get("bytes_per_launch")
     except (OSError, ValueError):
         pass
@@ -236,8 +257,9 @@ def cpu_baseline(torch, x, gate, up, down, topk_w, topk_i, wl, S):
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"first {S} of {wl['T']} tokens with all {wl['E']} experts' weights; candle-native "
-                  f"per-expert loop (oracle/oracle.c, per-op {wl['dtype']} rounding); {dt_s:.2f} s wall",
+        "sample": f"{'all' if S == wl['T'] else 'first'} {S} of {wl['T']} tokens with all {wl['E']} experts' "
+                  f"weights; candle-native per-expert loop (oracle/oracle.c, per-op {wl['dtype']} rounding); "
+                  f"{dt_s:.2f} s wall on {threads} threads",
     }
 
 

@@ -84,11 +84,15 @@ struct GemmArgs {
 // 2 stages.
 // kLds256w8 / kLds256w8k32: 256x256 with 8 waves (2 per SIMD), BK=64 2 stages
 // / BK=32 4 stages.
+// kPingPong: 256x256, 8 waves in two groups that alternate MFMA and memory
+// phases (moe_gemm_pp.hip).
+// kLds256w8k32s / kLds256k32s: 256x256, BK=32, 4 stages, 8 / 4 waves, with
+// each K tile's DMA spread over the k16 steps of the tile before it.
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
-    kLds256w8 = 7, kLds256w8k32 = 8
+    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11
 };
-constexpr int kNumTileCfgs = 9;
+constexpr int kNumTileCfgs = 12;
 inline int tile_rows(int cfg) {
     return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128) ? 128 : 256);
 }
@@ -102,6 +106,8 @@ bool mfma_supported(int dtype, int K, int N);
 int gemm_tile_cols(int mode, int cfg);
 hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
+hipError_t launch_moe_gemm_pp(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
+
 
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);

@@ -1,0 +1,221 @@
+// Device helpers shared by the LDS-DMA grouped GEMMs (moe_gemm_lds.hip,
+// moe_gemm_pp.hip): buffer resources, global->LDS DMA, explicit waits,
+// LDS swizzles, XCD-aware tile order and the per-tile epilogues.
+#pragma once
+
+#include "cm_common.hpp"
+#include "cm_internal.hpp"
+
+namespace cm {
+namespace lds {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+#define CM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every resource (operands are < 2 GiB)
+
+// Buffer resource (V#) of a raw byte range: base, stride 0, num_records =
+// bytes, dword3 0x00020000 (gfx9 data format); loads past num_records
+// return zeros. Made wave-uniform so it lives in SGPRs.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, long long bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)b);
+    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((b >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane((int32_t)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// One wave instruction: 64 lanes x 16 bytes from the buffer into LDS at
+// lds_off + 16*lane. Issued as inline asm so that the compiler neither waits
+// for it before unrelated LDS reads nor tracks it: stage hand-over is done
+// with the explicit s_waitcnt / s_barrier below.
+__device__ __forceinline__ void dma16(const i32x4& r, uint32_t lds_off, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_off), "v"(voff), "s"(r)
+                 : "memory");
+}
+// Same with a wave-uniform byte offset in an SGPR (address = base + voff +
+// soff). Used only where base + voff + soff stays inside the operand for
+// every lane whose voff is in range.
+__device__ __forceinline__ void dma16s(const i32x4& r, uint32_t lds_off, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_off), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" : : : "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)(p));
+}
+
+// Rows of K-contiguous tiles (A, [N,K] weights) hold ACH 16-byte chunks
+// (ACH = BK / 8); chunk c of row r is stored at a_swz(r, c). 16 lanes of a
+// ds_read_b128 read 16 consecutive rows at one logical chunk and land in 16
+// distinct bank groups.
+template <int ACH>
+__device__ __forceinline__ int a_swz(int r, int c) {
+    if constexpr (ACH == 8) return (c ^ r ^ (r >> 3)) & 7;
+    else return (c ^ (r >> 2)) & 3;
+}
+
+// [K,N] sub-tile rows of BCH 16-byte chunks: chunk c of k-row r is stored at
+// kn_swz(r, c). A transposed read touches 4 consecutive rows x 4 consecutive
+// chunks (c multiple of 4 first) per 32 lanes; the xor sends them to 16
+// distinct bank groups (rows are 256 B apart for BCH >= 16, 128 B for 8).
+template <int BCH>
+__device__ __forceinline__ int kn_swz(int r, int c) {
+    if constexpr (BCH >= 16) return c ^ ((r & 3) << 2);
+    else return c ^ (((r >> 1) & 1) << 2);
+}
+
+// Bijective remap of the hardware dispatch order (workgroup w runs on XCD
+// w % 8) to a logical tile id that is contiguous per XCD.
+__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
+    const int nwg = gridDim.x;
+    const int w = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
+    const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
+    mt = logical / n_tiles;
+    nt = logical - mt * n_tiles;
+}
+
+// Two ds_read_b64_tr_b16 results (k rows kr..kr+3 and kr+4..kr+7 of one
+// column) as the 8-value MFMA operand.
+__device__ __forceinline__ u32x4 tr_pair(const char* p_lo, const char* p_hi) {
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(CM_LDS(p_lo)));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(CM_LDS(p_hi)));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+    const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+    u32x4 v;
+    v[0] = l2[0];
+    v[1] = l2[1];
+    v[2] = h2[0];
+    v[3] = h2[1];
+    return v;
+}
+
+// Expert ids of the k slots of an expert-set key (base n_experts+1 digits,
+// most significant first) and the number of valid ones.
+__device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int (&seg_exp)[kSetMaxK]) {
+    const int base = n_experts + 1;
+    for (int s = k_top - 1; s >= 0; --s) {
+        seg_exp[s] = key % base;
+        key /= base;
+    }
+    int n = 0;
+    for (int s = 0; s < k_top; ++s) n += seg_exp[s] < n_experts;
+    return n;
+}
+
+// ------------------------------------------------------------------ epilogues
+// One wave's MB x NB blocks of 32x32 accumulators, the wave's sub-tile at
+// rows wm*WM, columns wn*WN of a BM x BN block tile (row tile r0, column
+// tile nt). Non-atomic modes were computed with swapped MFMA operands, so
+// lane l holds row l%32 and, in register group g = i/4, the 4 consecutive
+// columns 8g + 4(l/32) .. +3 of each 32-column block. Atomic modes were not
+// swapped: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32
+// (32 consecutive columns per atomic instruction).
+//  kGateUp / kFc1 : inter[dst] = dtype(w? * act(gate) (* up)), dst = pair_dest[p] or the sorted row
+//  kDownSet/kFc2Set: out[tok] = dtype(out[tok] + acc)  (each output row is owned by one tile)
+//  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
+template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
+                                              int wm, int wn, int lane, const int32_t* s_tok, const float* s_w) {
+    constexpr bool DUAL = (MODE == kGateUp);
+    constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
+    const int N = a.N;
+    const int lr = lane & 31, lh = lane >> 5;
+    if constexpr (ATOMIC) {
+        float* C = reinterpret_cast<float*>(a.C);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int ml = wm * WM + mb * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+                if (ml >= m_valid) continue;
+                const long long rowoff = (long long)s_tok[ml] * N;
+                const float w = s_w[ml];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int col = nt * BN + wn * WN + nb * 32 + lr;
+                    if (col < N) unsafeAtomicAdd(C + rowoff + col, w * acc[mb][nb][i]);
+                }
+            }
+        }
+    } else {
+        const int nsub = 4 * lh;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int ml = wm * WM + mb * 32 + lr;
+            if (ml >= m_valid) continue;
+            const int r = r0 + ml;
+            if constexpr (MODE == kGateUp || MODE == kFc1) {
+                const int p = a.sorted_pair[r];
+                const int dst = a.pair_dest ? a.pair_dest[p] : r;
+                const float wscale = a.fold_w ? a.routing_w[p] : 1.0f;
+                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)dst * N;
+                constexpr int PAIRS = DUAL ? NB / 2 : NB;
+#pragma unroll
+                for (int q = 0; q < PAIRS; ++q) {
+                    const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = colbase + 8 * g + nsub;
+                        if (col >= N) continue;
+                        float h[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            if constexpr (DUAL) {
+                                h[j] = act_fast(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
+                            } else {
+                                h[j] = act_fast(acc[mb][q][4 * g + j], a.act);
+                            }
+                            h[j] *= wscale;
+                        }
+                        u32x2 v;
+                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
+                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                        *reinterpret_cast<u32x2*>(C + col) = v;
+                    }
+                }
+            } else {
+                const int tok = a.tok_sorted[r];
+                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)tok * N;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int colbase = nt * BN + wn * WN + nb * 32;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = colbase + 8 * g + nsub;
+                        if (col >= N) continue;
+                        const u32x2 old = *reinterpret_cast<const u32x2*>(C + col);
+                        float h[4];
+                        h[0] = Elem<DT>::to_f32((uint16_t)(old[0] & 0xffffu)) + acc[mb][nb][4 * g + 0];
+                        h[1] = Elem<DT>::to_f32((uint16_t)(old[0] >> 16)) + acc[mb][nb][4 * g + 1];
+                        h[2] = Elem<DT>::to_f32((uint16_t)(old[1] & 0xffffu)) + acc[mb][nb][4 * g + 2];
+                        h[3] = Elem<DT>::to_f32((uint16_t)(old[1] >> 16)) + acc[mb][nb][4 * g + 3];
+                        u32x2 v;
+                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
+                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                        *reinterpret_cast<u32x2*>(C + col) = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace lds
+}  // namespace cm

@@ -23,90 +23,13 @@
 //                       SUBN*2 bytes (one per k), chunk c of row k stored at
 //                       kn_swz(k, c), so the 4 rows of a transposed read hit
 //                       disjoint banks.
-#include "cm_common.hpp"
-#include "cm_internal.hpp"
+#include "cm_lds.hpp"
 
 namespace cm {
 
-namespace {
+using namespace lds;
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-#define CM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every resource (operands are < 2 GiB)
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer resource (V#) of a raw byte range: base, stride 0, num_records =
-// bytes, dword3 0x00020000 (gfx9 data format); loads past num_records
-// return zeros. Made wave-uniform so it lives in SGPRs.
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, long long bytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    i32x4 r;
-    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)b);
-    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((b >> 32) & 0xffffu));
-    r[2] = __builtin_amdgcn_readfirstlane((int32_t)bytes);
-    r[3] = 0x00020000;
-    return r;
-}
-
-// One wave instruction: 64 lanes x 16 bytes from the buffer into LDS at
-// lds_off + 16*lane. Issued as inline asm so that the compiler neither waits
-// for it before unrelated LDS reads nor tracks it: stage hand-over is done
-// with the explicit s_waitcnt / s_barrier below.
-__device__ __forceinline__ void dma16(const i32x4& r, uint32_t lds_off, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_off), "v"(voff), "s"(r)
-                 : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
-__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" : : : "memory"); }
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)(p));
-}
-
-// Rows of K-contiguous tiles (A, [N,K] weights) hold ACH 16-byte chunks
-// (ACH = BK / 8); chunk c of row r is stored at a_swz(r, c). 16 lanes of a
-// ds_read_b128 read 16 consecutive rows at one logical chunk and land in 16
-// distinct bank groups.
-template <int ACH>
-__device__ __forceinline__ int a_swz(int r, int c) {
-    if constexpr (ACH == 8) return (c ^ r ^ (r >> 3)) & 7;
-    else return (c ^ (r >> 2)) & 3;
-}
-
-// [K,N] sub-tile rows of BCH 16-byte chunks: chunk c of k-row r is stored at
-// kn_swz(r, c). A transposed read touches 4 consecutive rows x 4 consecutive
-// chunks (c multiple of 4 first) per 32 lanes; the xor sends them to 16
-// distinct bank groups (rows are 256 B apart for BCH >= 16, 128 B for 8).
-template <int BCH>
-__device__ __forceinline__ int kn_swz(int r, int c) {
-    if constexpr (BCH >= 16) return c ^ ((r & 3) << 2);
-    else return c ^ (((r >> 1) & 1) << 2);
-}
-
-// Bijective remap of the hardware dispatch order (workgroup w runs on XCD
-// w % 8) to a logical tile id that is contiguous per XCD.
-__device__ __forceinline__ void lds_tile_coords(int n_tiles, int& mt, int& nt) {
-    const int nwg = gridDim.x;
-    const int w = blockIdx.x;
-    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
-    const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
-    mt = logical / n_tiles;
-    nt = logical - mt * n_tiles;
-}
-
-}  // namespace
-
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE>
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false>
 __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     // NW waves: 4 in a 2x2 layout (one per SIMD) or 8 in 2x4 (two per SIMD,
     // so one wave's MFMAs cover the other's LDS, DMA and VALU work)
@@ -149,7 +72,7 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     __shared__ float s_w[ATOMIC ? BM : 1];
 
     int mt, nt;
-    lds_tile_coords(a.n_tiles, mt, nt);
+    tile_coords(a.n_tiles, mt, nt);
     if (mt >= *a.num_tiles) return;
     const int r0 = a.tile_row[mt];
     const int grp = a.tile_exp[mt];
@@ -162,14 +85,7 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     int seg_exp[SET ? kSetMaxK : 1];
     int n_seg = 1;
     if constexpr (SET) {
-        const int base = a.n_experts + 1;
-        int key = grp;
-        n_seg = 0;
-        for (int s = a.k_top - 1; s >= 0; --s) {
-            seg_exp[s] = key % base;
-            key /= base;
-        }
-        for (int s = 0; s < a.k_top; ++s) n_seg += seg_exp[s] < a.n_experts;
+        n_seg = decode_set(grp, a.k_top, a.n_experts, seg_exp);
     } else {
         seg_exp[0] = grp;
     }
@@ -215,11 +131,14 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
         }
     }
 
-    auto issue = [&](int stage, int k0) {
+    // DMA instructions lo .. hi-1 of this wave's LOADS for the tile at k0
+    // (A instructions first, then B).
+    auto issue_range = [&](int stage, int k0, int lo, int hi) {
         const uint32_t sA = smem_base + stage * STAGE;
         const uint32_t sB = sA + A_BYTES;
 #pragma unroll
         for (int i = 0; i < A_INS; ++i) {
+            if (i < lo || i >= hi) continue;
             const int kc = k0 + a_kc[i];
             const uint32_t off = (a_row[i] == kOob || kc >= K) ? kOob : a_row[i] + (uint32_t)kc * 2u;
             dma16(rA, sA + (NW * i + wave) * 1024, off);
@@ -237,6 +156,7 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
         if constexpr (DUAL) r1s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B1) + eoff, a.strideB * 2);
 #pragma unroll
         for (int i = 0; i < B_INS; ++i) {
+            if (A_INS + i < lo || A_INS + i >= hi) continue;
             uint32_t off;
             if constexpr (BNK) {
                 const int kc = kk + b_r[i];
@@ -250,6 +170,7 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
             }
         }
     };
+    auto issue = [&](int stage, int k0) { issue_range(stage, k0, 0, LOADS); };
 
     f32x16 acc[MB][NB];
 #pragma unroll
@@ -294,16 +215,7 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
                 const int kr = kk * 16 + tr_k;  // kr & 3 == (tj >> 2); kr + 4 keeps the swizzle
                 const int cc = kn_swz<BCH>(kr, p >> 3);
                 const char* base = sB + (DUAL ? (nb & 1) * SUB_BYTES : 0) + cc * 16 + (p & 7) * 2;
-                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4*)(CM_LDS(base + kr * BROW)));
-                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4*)(CM_LDS(base + (kr + 4) * BROW)));
-                u32x4 v;
-                v[0] = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
-                v[1] = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
-                v[2] = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
-                v[3] = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
-                bfr[nb] = v;
+                bfr[nb] = tr_pair(base + kr * BROW, base + (kr + 4) * BROW);
             }
         }
     };
@@ -331,7 +243,18 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     };
     // KSTEPS k16 steps per stage; the fragments of step kk+1 are read while
     // the MFMAs of step kk run (two register sets).
-    auto compute = [&](int stage) {
+    // SPREAD: the DMA of the tile NST-1 ahead (stage ds, k0 dk; ds < 0: none)
+    // is issued in KSTEPS slices, one after each k16 step's MFMAs, so that a
+    // K tile's 64 KB reach the L2 at an even rate instead of in one burst
+    // that stalls the issuing waves.
+    constexpr int PER_STEP = (LOADS + KSTEPS - 1) / KSTEPS;
+    auto dma_slice = [&](int ds, int dk, int step) {
+        if constexpr (SPREAD) {
+            if (ds >= 0) issue_range(ds, dk, step * PER_STEP, (step + 1) * PER_STEP);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto compute = [&](int stage, int ds, int dk) {
         const char* sA = smem + stage * STAGE;
         const char* sB = sA + A_BYTES;
         u32x4 af0[MB], bf0[NB], af1[MB], bf1[NB];
@@ -341,18 +264,22 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
         mfma_step(af0, bf0);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, 0);
         if constexpr (KSTEPS == 4) {
             load_frags(sA, sB, 2, af0, bf0);
             mfma_step(af1, bf1);
             interleave();
             __builtin_amdgcn_sched_barrier(0);
+            dma_slice(ds, dk, 1);
             load_frags(sA, sB, 3, af1, bf1);
             mfma_step(af0, bf0);
             interleave();
             __builtin_amdgcn_sched_barrier(0);
+            dma_slice(ds, dk, 2);
         }
         mfma_step(af1, bf1);
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, KSTEPS - 1);
     };
 
     if constexpr (ATOMIC) {
@@ -386,89 +313,15 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
         wait_lgkm0();
         block_barrier();
         const int ahead = kt + NST - 1;
-        if (ahead < nk) issue(ahead % NST, ahead * BK);
-        compute(kt % NST);
+        if constexpr (SPREAD) {
+            compute(kt % NST, ahead < nk ? ahead % NST : -1, ahead * BK);
+        } else {
+            if (ahead < nk) issue(ahead % NST, ahead * BK);
+            compute(kt % NST, -1, 0);
+        }
     }
 
-    // ------------------------------------------------------------ epilogue
-    if constexpr (ATOMIC) {
-        float* C = reinterpret_cast<float*>(a.C);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int ml = wm * WM + mb * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
-                if (ml >= m_valid) continue;
-                const long long rowoff = (long long)s_tok[ml] * N;
-                const float w = s_w[ml];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const int col = nt * BN + wn * WN + nb * 32 + lr;
-                    if (col < N) unsafeAtomicAdd(C + rowoff + col, w * acc[mb][nb][i]);
-                }
-            }
-        }
-    } else {
-        const int nsub = 4 * lh;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            const int ml = wm * WM + mb * 32 + lr;
-            if (ml >= m_valid) continue;
-            const int r = r0 + ml;
-            if constexpr (MODE == kGateUp || MODE == kFc1) {
-                const int p = a.sorted_pair[r];
-                const int dst = a.pair_dest ? a.pair_dest[p] : r;
-                const float wscale = a.fold_w ? a.routing_w[p] : 1.0f;
-                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)dst * N;
-                constexpr int PAIRS = DUAL ? NB / 2 : NB;
-#pragma unroll
-                for (int q = 0; q < PAIRS; ++q) {
-                    const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int col = colbase + 8 * g + nsub;
-                        if (col >= N) continue;
-                        float h[4];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            if constexpr (DUAL) {
-                                h[j] = act_fast(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
-                            } else {
-                                h[j] = act_fast(acc[mb][q][4 * g + j], a.act);
-                            }
-                            h[j] *= wscale;
-                        }
-                        u32x2 v;
-                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
-                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
-                        *reinterpret_cast<u32x2*>(C + col) = v;
-                    }
-                }
-            } else {
-                const int tok = a.tok_sorted[r];
-                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)tok * N;
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const int colbase = nt * BN + wn * WN + nb * 32;
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int col = colbase + 8 * g + nsub;
-                        if (col >= N) continue;
-                        const u32x2 old = *reinterpret_cast<const u32x2*>(C + col);
-                        float h[4];
-                        h[0] = Elem<DT>::to_f32((uint16_t)(old[0] & 0xffffu)) + acc[mb][nb][4 * g + 0];
-                        h[1] = Elem<DT>::to_f32((uint16_t)(old[0] >> 16)) + acc[mb][nb][4 * g + 1];
-                        h[2] = Elem<DT>::to_f32((uint16_t)(old[1] & 0xffffu)) + acc[mb][nb][4 * g + 2];
-                        h[3] = Elem<DT>::to_f32((uint16_t)(old[1] >> 16)) + acc[mb][nb][4 * g + 3];
-                        u32x2 v;
-                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
-                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
-                        *reinterpret_cast<u32x2*>(C + col) = v;
-                    }
-                }
-            }
-        }
-    }
+    tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w);
 }
 
 template <int DT, int MODE>
@@ -497,6 +350,12 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
             case kLds256w8k32:
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
                 break;
+            case kLds256w8k32s:
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 8, MODE, true>), dim3(nwg), dim3(512), 0, stream, a);
+                break;
+            case kLds256k32s:
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 4, MODE, true>), dim3(nwg), dim3(256), 0, stream, a);
+                break;
             default:
                 return hipErrorInvalidValue;
         }
@@ -518,6 +377,7 @@ static hipError_t launch_lds_dt(int mode, int cfg, const GemmArgs& a, hipStream_
 }
 
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
+    if (cfg == kPingPong) return launch_moe_gemm_pp(mode, dtype, a, stream);
     if (dtype == kBF16) return launch_lds_dt<kBF16>(mode, cfg, a, stream);
     if (dtype == kF16) return launch_lds_dt<kF16>(mode, cfg, a, stream);
     return hipErrorInvalidValue;

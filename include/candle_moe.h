@@ -126,7 +126,10 @@ const char* candle_moe_profile_slot_name(int slot);
 int candle_moe_set_combine_policy(int policy);
 /* GEMM kernel of fused_moe (process-wide): 0 = choose per call (default);
  * register-staged MFMA kernels 1 = 128x128, 2 = 256x256 block tiles;
- * LDS-DMA MFMA kernels 3 = 256x256, 4 = 256x128, 5 = 128x128. */
+ * LDS-DMA MFMA kernels 3 = 256x256 (BK 32), 4 = 256x128, 5 = 128x128,
+ * 6 = 256x256 (BK 64, 4 waves), 7 = 256x256 (8 waves), 8 = 256x256 (8 waves,
+ * BK 32), 9 = 256x256 (8 waves alternating MFMA and memory phases),
+ * 10 / 11 = 256x256 BK 32 with the DMA spread over the K loop, 8 / 4 waves. */
 int candle_moe_set_tile_policy(int policy);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
