@@ -111,12 +111,16 @@ struct Problem {
     long long P;
     bool set_path;  // expert-set down projection (no atomics, no f32 accumulator)
     int nkeys;      // (E+1)^k expert-set keys
+    int split1;     // K splits of the gate/up GEMM (moe_lds_gemm only; > 1 needs partial + counters)
+    int split2;     // K splits of the pair-path down GEMM (atomic combine)
+    int n_tiles1, n_tiles2;
+    bool lds_family;  // both GEMMs run moe_lds_gemm (fused clears and K splits available)
 };
 
 struct Layout {
     size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles;
     size_t k_offsets, k_block_counts, tok_sorted, tile_row2, tile_key2, num_tiles2, pair_dest;
-    size_t inter, acc, total;
+    size_t inter, acc, partial, counters, total;
 };
 
 // 0: choose per call; 1: always the pair path (f32 atomics); 2: the
@@ -159,6 +163,17 @@ static Layout make_layout(const Problem& p) {
     L.inter = o; o += a256((size_t)p.P * p.I * es);
     L.acc = o;
     if (!p.set_path) o += a256((size_t)p.T * p.H * 4);
+    // split-K partials and arrival counters, shared by the two GEMMs (they run
+    // one after the other; the counters are left zero)
+    L.partial = L.counters = o;
+    if (p.split1 > 1 || p.split2 > 1) {
+        const size_t t1 = (size_t)mt * p.n_tiles1 * (p.split1 > 1 ? p.split1 : 0);
+        const size_t t2 = (size_t)mt * p.n_tiles2 * (p.split2 > 1 ? p.split2 : 0);
+        const size_t c1 = p.split1 > 1 ? (size_t)mt * p.n_tiles1 : 0;
+        const size_t c2 = p.split2 > 1 ? (size_t)mt * p.n_tiles2 : 0;
+        L.partial = o; o += a256((t1 > t2 ? t1 : t2) * p.BM * tile_cols(p.cfg) * 4);
+        L.counters = o; o += a256((c1 > c2 ? c1 : c2) * 4);
+    }
     L.total = o;
     return L;
 }
@@ -181,8 +196,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.P = P;
     p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
     // Default MFMA kernel: LDS-DMA, 256x256 block tile, 8 waves (measured
-    // fastest on every BASELINE shape, including the skewed E=128 one).
+    // fastest on every BASELINE shape from a few hundred rows per expert up,
+    // including the skewed E=128 one). With at most 32 rows per touched expert
+    // on average (decode) the GEMMs stream each touched expert's weights once
+    // and the 32-row tile keeps the padding and the MFMA work small.
     p.cfg = !p.mfma ? kTileSimt : (g_tile_policy ? g_tile_policy : kLds256w8);
+    if (p.mfma && !g_tile_policy) {
+        const long long touched = P < E ? P : E;
+        if (P <= 32 * touched) p.cfg = kLdsRows32;
+    }
     // the LDS-DMA kernels address operands with 32-bit buffer offsets
     if (is_lds_cfg(p.cfg)) {
         const long long es = 2;
@@ -203,22 +225,53 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             for (int j = 0; j < k; ++j) sets = sets * (E - j) / (j + 1);
             if (sets < 1.0) sets = 1.0;
             p.nkeys = (int)nk;
-            p.set_path = g_combine_policy == 2 || (double)T >= 0.5 * p.BM * sets;
+            p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= 0.5 * p.BM * sets);
         }
+    }
+    // K splits for the 32-row (decode) GEMMs whose output tiles leave most
+    // CUs idle (< 64 tiles): up to ~256 workgroups, at most 8 splits, no empty
+    // split. Each split writes a 32 KB f32 partial that the last one sums, so
+    // splitting only pays where the weight stream would otherwise run on a
+    // few CUs.
+    p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
+    p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
+    p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
+    p.split1 = p.split2 = 1;
+    if (p.lds_family && p.cfg == kLdsRows32 && P > 0) {
+        const long long mt = grouping_max_tiles(P, E, p.BM);
+        const int bk = tile_bk(p.cfg);
+        auto choose = [&](long long tiles, int K) {
+            if (tiles >= 64) return 1;
+            const int nk = (K + bk - 1) / bk;
+            long long sp = (256 + tiles - 1) / tiles;
+            if (sp > 8) sp = 8;
+            if (sp > nk) sp = nk;
+            if (sp < 1) sp = 1;
+            const int per = (int)((nk + sp - 1) / sp);
+            return (nk + per - 1) / per;
+        };
+        if (!p.set_path) p.split2 = choose(mt * p.n_tiles2, I);
+        p.split1 = choose(mt * p.n_tiles1, H);
     }
     return CANDLE_MOE_OK;
 }
 
 static int run_moe(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
-                   const float* rw, const uint32_t* idx, void* out, char* ws, hipStream_t s) {
+                   const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, hipStream_t s) {
     const Layout L = make_layout(p);
-    GroupingBufs gb;
+    GroupingBufs gb = {};
     gb.offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
     gb.block_counts = reinterpret_cast<int32_t*>(ws + L.block_counts);
     gb.sorted_pair = reinterpret_cast<int32_t*>(ws + L.sorted_pair);
     gb.tile_row = reinterpret_cast<int32_t*>(ws + L.tile_row);
     gb.tile_exp = reinterpret_cast<int32_t*>(ws + L.tile_exp);
     gb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles);
+    int32_t* counters = reinterpret_cast<int32_t*>(ws + L.counters);
+    if (p.split1 > 1 || p.split2 > 1) {
+        const long long mt = grouping_max_tiles(p.P, p.E, p.BM);
+        gb.zero_ptr = counters;
+        gb.zero_n = (int)(mt * (p.n_tiles1 > p.n_tiles2 ? p.n_tiles1 : p.n_tiles2));
+    }
     hipError_t e;
     {
         ProfScope ps(kSlotGroup, s);
@@ -265,8 +318,17 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.k_top = p.k;
     g1.act = p.act;
     const int mode1 = qwen3 ? kGateUp : kFc1;
-    g1.n_tiles = cdiv(p.I, gemm_tile_cols(mode1, p.cfg));
+    g1.n_tiles = p.n_tiles1;
     g1.m_tiles_max = m_tiles_max;
+    g1.ksplit = p.split1;
+    g1.partial = reinterpret_cast<float*>(ws + L.partial);
+    g1.counters = counters;
+    // the gate/up workgroups clear the pair path's accumulator
+    const bool fused_clear = !p.set_path && p.lds_family;
+    if (fused_clear) {
+        g1.zero_f32 = acc;
+        g1.zero_n = (long long)p.T * p.H;
+    }
     g1.a_bytes = (long long)p.T * p.H * (p.dtype == kF32 ? 4 : 2);
     g1.pair_dest = pair_dest;
     g1.fold_w = p.set_path ? 1 : 0;
@@ -297,6 +359,10 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.tok_sorted = tb.sorted_pair;
         g2.pair_dest = nullptr;
         g2.fold_w = 0;
+        g2.ksplit = 1;
+        g2.zero_f32 = nullptr;
+        g2.zero_n = 0;
+        g2.overwrite = overwrite ? 1 : 0;
         const int mode2 = qwen3 ? kDownSet : kFc2Set;
         g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.cfg));
         g2.m_tiles_max = (int)set_tiles_max(p);
@@ -308,11 +374,11 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         return CANDLE_MOE_OK;
     }
 
-    {
+    if (!fused_clear) {
         ProfScope ps(kSlotZero, s);
         e = launch_fill_zero_f32(acc, (long long)p.T * p.H, s);
+        if (e != hipSuccess) return hip_fail(e, "fused_moe accumulator clear");
     }
-    if (e != hipSuccess) return hip_fail(e, "fused_moe accumulator clear");
 
     GemmArgs g2 = g1;
     g2.A = inter;
@@ -325,7 +391,12 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.N = p.H;
     g2.a_bytes = p.P * p.I * (p.dtype == kF32 ? 4 : 2);
     const int mode2 = qwen3 ? kDown : kFc2;
-    g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.cfg));
+    g2.n_tiles = p.n_tiles2;
+    g2.ksplit = p.split2;
+    g2.partial = reinterpret_cast<float*>(ws + L.partial);
+    g2.counters = counters;
+    g2.zero_f32 = nullptr;
+    g2.zero_n = 0;
     {
         ProfScope ps(kSlotGemm2, s);
         e = launch_moe_gemm(mode2, p.dtype, p.cfg, g2, s);
@@ -334,7 +405,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
 
     {
         ProfScope ps(kSlotFinal, s);
-        e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, s);
+        e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, overwrite, s);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe finalize");
     return CANDLE_MOE_OK;
@@ -369,7 +440,7 @@ static void prepare_pool_once() {
 
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
-                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, void* stream) {
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream) {
     clear_error();
     Problem p;
     int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p);
@@ -386,7 +457,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
         if ((uintptr_t)ws % 256)
             return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: workspace must be 256-byte aligned");
         return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw),
-                       reinterpret_cast<const uint32_t*>(idx), out, reinterpret_cast<char*>(ws), s);
+                       reinterpret_cast<const uint32_t*>(idx), out, overwrite, reinterpret_cast<char*>(ws), s);
     }
     prepare_pool_once();
     void* mem = nullptr;
@@ -394,7 +465,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
     if (e != hipSuccess) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s",
                                           L.total, hipGetErrorString(e));
     rc = run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                 out, reinterpret_cast<char*>(mem), s);
+                 out, overwrite, reinterpret_cast<char*>(mem), s);
     e = hipFreeAsync(mem, s);
     if (rc == CANDLE_MOE_OK && e != hipSuccess) return hip_fail(e, "fused_moe: hipFreeAsync");
     return rc;
@@ -439,7 +510,7 @@ void fused_moe(const void* input, const void* gate_weights, const void* up_weigh
                uint32_t moe_type, uint32_t dtype, void* stream) {
     (void)cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
                              num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
-                             activation_type, moe_type, dtype, nullptr, 0, true, stream);
+                             activation_type, moe_type, dtype, nullptr, 0, true, false, stream);
 }
 
 int candle_moe_fused_moe_status(const void* input, const void* gate_weights, const void* up_weights,
@@ -449,7 +520,7 @@ int candle_moe_fused_moe_status(const void* input, const void* gate_weights, con
                                 void* stream) {
     return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
                               num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
-                              activation_type, moe_type, dtype, nullptr, 0, true, stream);
+                              activation_type, moe_type, dtype, nullptr, 0, true, false, stream);
 }
 
 size_t candle_moe_fused_moe_workspace_size(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
@@ -464,7 +535,7 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
                             void* workspace, size_t workspace_bytes, void* stream) {
     return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
                               num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
-                              activation_type, moe_type, dtype, workspace, workspace_bytes, false, stream);
+                              activation_type, moe_type, dtype, workspace, workspace_bytes, false, false, stream);
 }
 
 const char* candle_moe_last_error(void) { return cm::g_last_error.c_str(); }

@@ -22,10 +22,14 @@ struct GroupingBufs {
     int32_t* tile_row;      // [max_tiles]: first sorted row of the tile
     int32_t* tile_exp;      // [max_tiles]: expert of the tile
     int32_t* num_tiles;     // [1]
+    int32_t* zero_ptr;      // ints cleared before the GEMMs run (may be null)
+    int zero_n;
 };
 constexpr int kGroupChunk = 4096;  // pairs per grouping workgroup
 inline int grouping_blocks(long long P) { return (int)((P + kGroupChunk - 1) / kGroupChunk); }
-inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM - 1) / BM + E; }
+// Row tiles of a grouping: sum over non-empty groups of ceil(count / BM)
+// <= ceil(P / BM) + (number of non-empty groups).
+inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM - 1) / BM + (P < E ? P : E); }
 hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
                            hipStream_t stream);
 
@@ -74,6 +78,13 @@ struct GemmArgs {
     int n_experts;            // E (key digits are base E+1)
     int seg_len;              // set GEMM2: K length of one slot's segment (= I)
     long long a_bytes;        // size of A in bytes (LDS-DMA kernels: buffer range, < 2^31)
+    // split-K and fused clears (moe_lds_gemm only)
+    int ksplit;               // workgroups per output tile along K (<= 1: one)
+    float* partial;           // non-atomic modes with ksplit > 1: [m_tiles_max*n_tiles][ksplit][BM*BN] f32
+    int32_t* counters;        // [m_tiles_max*n_tiles] arrival counters: zero on entry, left zero
+    float* zero_f32;          // f32 range cleared by this launch's workgroups (null: none)
+    long long zero_n;
+    int overwrite;            // expert-set down GEMM: out = acc instead of out + acc
 };
 
 // Kernel shapes. kTileSimt: 64x64 SIMT; kTile128 / kTile256: MFMA kernels
@@ -88,18 +99,25 @@ struct GemmArgs {
 // phases (moe_gemm_pp.hip).
 // kLds256w8k32s / kLds256k32s: 256x256, BK=32, 4 stages, 8 / 4 waves, with
 // each K tile's DMA spread over the k16 steps of the tile before it.
+// kLdsRows32: 32x256 block tile, 4 waves side by side along N, BK=64,
+// 4 stages: few rows per expert (decode), bound by streaming the weights.
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
-    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11
+    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11, kLdsRows32 = 12
 };
-constexpr int kNumTileCfgs = 12;
+constexpr int kNumTileCfgs = 13;
 inline int tile_rows(int cfg) {
+    if (cfg == kLdsRows32) return 32;
     return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128) ? 128 : 256);
 }
 inline int tile_cols(int cfg) {
     return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128) ? 128 : 256);
 }
 inline bool is_lds_cfg(int cfg) { return cfg >= kLds256; }
+// K tile of the LDS-DMA kernels
+inline int tile_bk(int cfg) {
+    return (cfg == kLds256 || cfg == kLds256w8k32 || cfg == kLds256w8k32s || cfg == kLds256k32s) ? 32 : 64;
+}
 
 bool mfma_supported(int dtype, int K, int N);
 // Logical output columns covered by one workgroup of the chosen kernel.
@@ -112,8 +130,8 @@ hipError_t launch_moe_gemm_pp(int mode, int dtype, const GemmArgs& a, hipStream_
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);
 hipError_t launch_fill_zero_bytes(void* p, long long nbytes, hipStream_t stream);
-// out[i] = dtype(out[i] + acc[i])
-hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, hipStream_t stream);
+// out[i] = dtype(out[i] + acc[i]), or dtype(acc[i]) with overwrite
+hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, bool overwrite, hipStream_t stream);
 
 // ------------------------------------------------------------ C-ABI core
 // Record the message of a failing call (thread-local) and return `code`.
@@ -123,6 +141,6 @@ int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void*
                       void* stream);
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
-                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, void* stream);
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream);
 
 }  // namespace cm

@@ -81,14 +81,33 @@ __device__ __forceinline__ int kn_swz(int r, int c) {
 }
 
 // Bijective remap of the hardware dispatch order (workgroup w runs on XCD
-// w % 8) to a logical tile id that is contiguous per XCD.
-__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
+// w % 8) to a logical id that is contiguous per XCD.
+__device__ __forceinline__ int logical_wg() {
     const int nwg = gridDim.x;
     const int w = blockIdx.x;
     const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
-    const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
+    const int logical = logical_wg();
     mt = logical / n_tiles;
     nt = logical - mt * n_tiles;
+}
+
+// Clear this workgroup's share of n floats at p (16-byte stores where p is
+// 16-byte aligned, which the workspace guarantees).
+__device__ __forceinline__ void clear_share(float* p, long long n) {
+    if (!p || n <= 0) return;
+    const long long per = ((n + gridDim.x - 1) / gridDim.x + 3) & ~3LL;
+    const long long lo = (long long)blockIdx.x * per;
+    const long long hi = lo + per < n ? lo + per : n;
+    for (long long i = lo + 4LL * threadIdx.x; i < hi; i += 4LL * blockDim.x) {
+        if (i + 4 <= hi) {
+            *reinterpret_cast<f32x4*>(p + i) = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            for (long long j = i; j < hi; ++j) p[j] = 0.f;
+        }
+    }
 }
 
 // Two ds_read_b64_tr_b16 results (k rows kr..kr+3 and kr+4..kr+7 of one
@@ -104,6 +123,54 @@ __device__ __forceinline__ u32x4 tr_pair(const char* p_lo, const char* p_hi) {
     v[2] = h2[0];
     v[3] = h2[1];
     return v;
+}
+
+// Split-K fixup. Every split writes its f32 partial tile to
+// a.partial[tile][ks] (lane-contiguous per register), then counts itself in
+// a.counters[tile]; the split that arrives last sums all partials in split
+// order (so the result does not depend on which split finished last), resets
+// the counter and returns true (it runs the epilogue, once per tile), the
+// others return false. The splits may run on different XCDs, whose L2s are
+// not coherent with each other: the partials are written and read with
+// device-scope relaxed atomics (write-through / L2-bypassing accesses), each
+// thread waits for its stores before the workgroup counts itself, so no
+// L2-wide write-back or invalidate is needed.
+template <int MB, int NB, int NW>
+__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB][NB], int tile, int ks,
+                                             int nsplit, int wave, int lane) {
+    __shared__ int s_last;
+    constexpr int PER_WAVE = MB * NB * 16 * 64;
+    constexpr int PER = NW * PER_WAVE;  // floats per workgroup partial (BM * BN)
+    float* mine = a.partial + ((long long)tile * nsplit + ks) * PER + wave * PER_WAVE;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                __hip_atomic_store(mine + ((mb * NB + nb) * 16 + i) * 64 + lane, acc[mb][nb][i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    __syncthreads();
+    if (!s_last) return false;
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+        float* o = a.partial + ((long long)tile * nsplit + s2) * PER + wave * PER_WAVE;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float v = __hip_atomic_load(o + ((mb * NB + nb) * 16 + i) * 64 + lane, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    acc[mb][nb][i] = s2 == 0 ? v : acc[mb][nb][i] + v;
+                }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
 }
 
 // Expert ids of the k slots of an expert-set key (base n_experts+1 digits,
@@ -128,7 +195,8 @@ __device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int
 // swapped: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32
 // (32 consecutive columns per atomic instruction).
 //  kGateUp / kFc1 : inter[dst] = dtype(w? * act(gate) (* up)), dst = pair_dest[p] or the sorted row
-//  kDownSet/kFc2Set: out[tok] = dtype(out[tok] + acc)  (each output row is owned by one tile)
+//  kDownSet/kFc2Set: out[tok] = dtype(out[tok] + acc), or dtype(acc) with overwrite
+//                   (each output row is owned by one tile)
 //  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
 template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
@@ -200,7 +268,9 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                     for (int g = 0; g < 4; ++g) {
                         const int col = colbase + 8 * g + nsub;
                         if (col >= N) continue;
-                        const u32x2 old = *reinterpret_cast<const u32x2*>(C + col);
+                        // overwrite: add to +0 instead of the old value (no read)
+                        u32x2 old = {0u, 0u};
+                        if (!a.overwrite) old = *reinterpret_cast<const u32x2*>(C + col);
                         float h[4];
                         h[0] = Elem<DT>::to_f32((uint16_t)(old[0] & 0xffffu)) + acc[mb][nb][4 * g + 0];
                         h[1] = Elem<DT>::to_f32((uint16_t)(old[0] >> 16)) + acc[mb][nb][4 * g + 1];

@@ -186,9 +186,141 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t
     }
 }
 
+// Exclusive scan of v[0..n) in place (one workgroup of kGroupThreads),
+// returning the total; s_part is kGroupThreads ints of scratch. Each thread
+// scans a contiguous run of ceil(n / threads) entries.
+__device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
+    const int per = (n + kGroupThreads - 1) / kGroupThreads;
+    const int lo = threadIdx.x * per;
+    const int hi = lo + per < n ? lo + per : n;
+    int32_t run = 0;
+    for (int i = lo; i < hi; ++i) run += v[i];
+    s_part[threadIdx.x] = run;
+    __syncthreads();
+    // Hillis-Steele over the per-thread sums
+    for (int d = 1; d < kGroupThreads; d <<= 1) {
+        const int32_t add = threadIdx.x >= d ? s_part[threadIdx.x - d] : 0;
+        __syncthreads();
+        s_part[threadIdx.x] += add;
+        __syncthreads();
+    }
+    const int32_t total = s_part[kGroupThreads - 1];
+    int32_t base = s_part[threadIdx.x] - run;
+    for (int i = lo; i < hi; ++i) {
+        const int32_t c = v[i];
+        v[i] = base;
+        base += c;
+    }
+    __syncthreads();
+    return total;
+}
+
+// All of grouping in one workgroup, for at most kGroupChunk items: LDS
+// histogram, block-wide scans of the counts and of the per-bin tile counts,
+// the tile table, and the stable ballot scatter. Also clears zero_n ints at
+// zero_ptr (the split-K arrival counters of the GEMMs that follow).
+template <bool TOK>
+__global__ __launch_bounds__(kGroupThreads) void grouping_small(const uint32_t* __restrict__ idx, int P, int k,
+                                                                int E, int nbins, int ebits, int BM,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ sorted_pair,
+                                                                int32_t* __restrict__ tile_row,
+                                                                int32_t* __restrict__ tile_exp,
+                                                                int32_t* __restrict__ num_tiles,
+                                                                int32_t* __restrict__ pair_dest,
+                                                                int32_t* __restrict__ zero_ptr, int zero_n) {
+    extern __shared__ int32_t s_mem[];
+    int32_t* s_cnt = s_mem;               // [4][nbins] per-wave histogram, then per-wave step counts
+    int32_t* s_off = s_mem + 4 * nbins;   // [nbins] bin offsets -> running positions
+    int32_t* s_tb = s_off + nbins;        // [nbins] tile bases
+    int32_t* s_part = s_tb + nbins;       // [kGroupThreads] scan scratch
+    __shared__ int32_t s_max;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
+    for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
+    if (threadIdx.x == 0) s_max = 0;
+    __syncthreads();
+    int rank[kSetMaxK];
+    for (int p = threadIdx.x; p < P; p += kGroupThreads) {
+        const int b = item_bin<TOK>(idx, p, k, E, rank);
+        if (b >= 0) atomicAdd(s_cnt + wave * nbins + b, 1);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+        const int32_t c = s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
+        s_off[e] = c;
+        s_tb[e] = (c + BM - 1) / BM;
+        atomicMax(&s_max, c);
+        s_cnt[e] = s_cnt[nbins + e] = s_cnt[2 * nbins + e] = s_cnt[3 * nbins + e] = 0;
+    }
+    __syncthreads();
+    const int32_t total = block_exclusive_scan(s_off, nbins, s_part);
+    const int32_t tiles = block_exclusive_scan(s_tb, nbins, s_part);
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+        offsets[e] = s_off[e];
+        const int32_t c = (e + 1 < nbins ? s_off[e + 1] : total) - s_off[e];
+        const int32_t nt = (c + BM - 1) / BM;
+        for (int i = 0; i < nt; ++i) {
+            tile_row[s_tb[e] + i] = s_off[e] + i * BM;
+            tile_exp[s_tb[e] + i] = e;
+        }
+    }
+    if (threadIdx.x == 0) {
+        offsets[nbins] = total;
+        offsets[nbins + 1] = s_max;
+        *num_tiles = tiles;
+    }
+    __syncthreads();
+    // stable scatter: s_off[e] is the next free position of bin e
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int s0 = 0; s0 < P; s0 += kGroupThreads) {
+        const int p = s0 + threadIdx.x;
+        const int bin = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        const bool active = bin >= 0;
+        const uint32_t e = active ? (uint32_t)bin : 0xffffffffu;
+        uint64_t peers = __ballot(active);
+        for (int b = 0; b < ebits; ++b) {
+            const bool bit = (e >> b) & 1u;
+            const uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        const int lrank = __popcll(peers & lt_mask);
+        if (active && lrank == 0) s_cnt[wave * nbins + e] = __popcll(peers);
+        __syncthreads();
+        if (active) {
+            int32_t pos = s_off[e] + lrank;
+            for (int w = 0; w < wave; ++w) pos += s_cnt[w * nbins + e];
+            sorted_pair[pos] = p;
+            if constexpr (TOK) {
+                for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
+            }
+        }
+        __syncthreads();
+        for (int ee = threadIdx.x; ee < nbins; ee += kGroupThreads) {
+            s_off[ee] += s_cnt[ee] + s_cnt[nbins + ee] + s_cnt[2 * nbins + ee] + s_cnt[3 * nbins + ee];
+            s_cnt[ee] = s_cnt[nbins + ee] = s_cnt[2 * nbins + ee] = s_cnt[3 * nbins + ee] = 0;
+        }
+        __syncthreads();
+    }
+}
+
 template <bool TOK>
 static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int E, int nbins, int BM,
                                 const GroupingBufs& b, int32_t* pair_dest, hipStream_t stream) {
+    int bbits0 = 0;
+    while ((1 << bbits0) < nbins) ++bbits0;
+    // LDS of the one-workgroup path: 6 * nbins + threads ints
+    if (items <= kGroupChunk && (6LL * nbins + kGroupThreads) * 4 <= 64 * 1024) {
+        hipLaunchKernelGGL((grouping_small<TOK>), dim3(1), dim3(kGroupThreads),
+                           (6 * nbins + kGroupThreads) * sizeof(int32_t), stream, idx, (int)items, k, E, nbins, bbits0,
+                           BM, b.offsets, b.sorted_pair, b.tile_row, b.tile_exp, b.num_tiles, pair_dest, b.zero_ptr,
+                           b.zero_n);
+        return hipGetLastError();
+    }
+    if (b.zero_n > 0) {
+        hipError_t e = launch_fill_zero_bytes(b.zero_ptr, (long long)b.zero_n * 4, stream);
+        if (e != hipSuccess) return e;
+    }
     const int nb = grouping_blocks(items);
     int bbits = 0;
     while ((1 << bbits) < nbins) ++bbits;

@@ -230,17 +230,13 @@ int candle_moe_fused_moe_forward(const cm_fused_moe_t* m, const cm_tensor_t* x, 
     if (!out) return cm::set_error(CANDLE_MOE_ERR_INVALID, "output is missing");
     int rc = cm::validate_moe(m, x, gate, up, down, rw, idx, moe_type, out);
     if (rc) return rc;
-    const int esz = x->dtype == CM_DT_F32 ? 4 : 2;
-    const long long bytes = out->dims[0] * out->dims[1] * esz;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // Tensor::zeros((num_tokens, hidden_dim)) of lib.rs:296, as a fill kernel
-    // (no hipMemsetAsync, so the call stays capturable).
-    const hipError_t e = cm::launch_fill_zero_bytes(out->data, bytes, s);
-    if (e != hipSuccess) return cm::set_error(CANDLE_MOE_ERR_HIP, "output clear: %s", hipGetErrorString(e));
+    // The reference zeroes a fresh output and accumulates into it
+    // (lib.rs:296); here the last kernel writes every element of out instead
+    // (overwrite), which gives the same tensor without the clear.
     return cm::fused_moe_impl(x->data, gate->data, up->data, down ? down->data : nullptr, rw->data, idx->data,
                               out->data, (int)x->dims[0], (int)x->dims[1], (int)gate->dims[2], (int)m->num_experts,
                               (int)m->num_selected_experts, m->activation, moe_type, (uint32_t)x->dtype, nullptr, 0,
-                              true, stream);
+                              true, true, stream);
 }
 
 }  // extern "C"

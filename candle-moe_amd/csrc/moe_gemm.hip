@@ -13,6 +13,7 @@
 // grouped by the sorted set of their k experts, GEMM1 writes w_p * h for
 // pair p into slot rank(j) of its token's row of inter [T, k*I], and
 //   kDownSet / kFc2Set : out[t] += [w h_1 | .. | w h_k] . [B_e1; ..; B_ek]
+//                        (out[t] = ... with a.overwrite)
 // one GEMM over K = k*I whose weight block switches expert every I rows, so
 // each output row is written exactly once: no atomics, no f32 accumulator.
 //
@@ -341,7 +342,9 @@ __global__ __launch_bounds__(256, 1) void moe_mfma_gemm(GemmArgs a) {
                     for (int g = 0; g < 4; ++g) {
                         const int col = colbase + 8 * g + nsub;
                         if (col >= N) continue;
-                        const u32x2 old = *reinterpret_cast<const u32x2*>(C + col);
+                        // overwrite: add to +0 instead of the old value (no read)
+                        u32x2 old = {0u, 0u};
+                        if (!a.overwrite) old = *reinterpret_cast<const u32x2*>(C + col);
                         float h[4];
                         h[0] = Elem<DT>::to_f32((uint16_t)(old[0] & 0xffffu)) + acc[mb][nb][4 * g + 0];
                         h[1] = Elem<DT>::to_f32((uint16_t)(old[0] >> 16)) + acc[mb][nb][4 * g + 1];
@@ -468,10 +471,10 @@ __global__ void fill_zero_u32x4(u32x4* __restrict__ p, long long n) {
 
 template <int DT>
 __global__ void finalize_kernel(typename Elem<DT>::storage* __restrict__ out, const float* __restrict__ acc,
-                                long long n) {
+                                long long n, int overwrite) {
     const long long stride = (long long)gridDim.x * blockDim.x;
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        out[i] = Elem<DT>::from_f32(Elem<DT>::to_f32(out[i]) + acc[i]);
+        out[i] = Elem<DT>::from_f32(overwrite ? acc[i] : Elem<DT>::to_f32(out[i]) + acc[i]);
 }
 
 static unsigned grid_for(long long n, int block) {
@@ -509,15 +512,16 @@ hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream) {
     return launch_fill_zero_bytes(p, n * 4, stream);
 }
 
-hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, hipStream_t stream) {
+hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, bool overwrite, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const dim3 g(grid_for(n, 256)), b(256);
+    const int ow = overwrite ? 1 : 0;
     if (dtype == kBF16)
-        hipLaunchKernelGGL(finalize_kernel<kBF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n);
+        hipLaunchKernelGGL(finalize_kernel<kBF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n, ow);
     else if (dtype == kF16)
-        hipLaunchKernelGGL(finalize_kernel<kF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n);
+        hipLaunchKernelGGL(finalize_kernel<kF16>, g, b, 0, stream, reinterpret_cast<uint16_t*>(out), acc, n, ow);
     else
-        hipLaunchKernelGGL(finalize_kernel<kF32>, g, b, 0, stream, reinterpret_cast<float*>(out), acc, n);
+        hipLaunchKernelGGL(finalize_kernel<kF32>, g, b, 0, stream, reinterpret_cast<float*>(out), acc, n, ow);
     return hipGetLastError();
 }
 

@@ -29,13 +29,17 @@ namespace cm {
 
 using namespace lds;
 
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false>
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false, int WGM = 2>
 __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
-    // NW waves: 4 in a 2x2 layout (one per SIMD) or 8 in 2x4 (two per SIMD,
-    // so one wave's MFMAs cover the other's LDS, DMA and VALU work)
+    // NW waves in WGM rows: 4 in a 2x2 layout (one per SIMD), 8 in 2x4 (two
+    // per SIMD, so one wave's MFMAs cover the other's LDS, DMA and VALU work),
+    // or all side by side along N (WGM = 1) for 32-row tiles, where the
+    // weight panels dominate and the row block is shared by every wave.
     static_assert(NW == 4 || NW == 8, "waves");
-    constexpr int WGN = NW / 2;
-    constexpr int WM = BM / 2, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+    static_assert(WGM == 1 || WGM == 2, "wave rows");
+    constexpr int WGN = NW / WGM;
+    constexpr int WM = BM / WGM, WN = BN / WGN, MB = WM / 32, NB = WN / 32;
+    static_assert(MB >= 1 && NB >= 1, "wave tile");
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
     constexpr bool SET = (MODE == kDownSet || MODE == kFc2Set);
@@ -71,8 +75,13 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     __shared__ int32_t s_tok[ATOMIC ? BM : 1];
     __shared__ float s_w[ATOMIC ? BM : 1];
 
-    int mt, nt;
-    tile_coords(a.n_tiles, mt, nt);
+    // workgroup -> (output tile, K split); every workgroup first clears its
+    // share of zero_f32 (the accumulator of the GEMM that follows)
+    clear_share(a.zero_f32, a.zero_n);
+    const int nsplit = a.ksplit > 1 ? a.ksplit : 1;
+    const int lg = logical_wg();
+    const int tile = lg / nsplit, ks = lg - tile * nsplit;
+    const int mt = tile / a.n_tiles, nt = tile - mt * a.n_tiles;
     if (mt >= *a.num_tiles) return;
     const int r0 = a.tile_row[mt];
     const int grp = a.tile_exp[mt];
@@ -294,10 +303,15 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     // stage kt (the NST-2 newer stages may stay in flight) and for its own
     // LDS reads of stage kt-1, then the barrier makes both block-wide; only
     // after it is stage kt-1's slot refilled with tile kt+NST-1.
-    const int nk = (K + BK - 1) / BK;
+    // this split's K tiles: [kt0, kt0 + nk) of nk_all
+    const int nk_all = (K + BK - 1) / BK;
+    const int per_split = (nk_all + nsplit - 1) / nsplit;
+    const int kt0 = min(nk_all, ks * per_split);
+    const int nk = min(nk_all, kt0 + per_split) - kt0;
+
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
-        if (s < nk) issue(s, s * BK);
+        if (s < nk) issue(s, (kt0 + s) * BK);
     for (int kt = 0; kt < nk; ++kt) {
         const int newer = min(NST - 2, nk - 1 - kt);  // stages issued after kt and before this wait
         if constexpr (NST >= 4) {
@@ -314,19 +328,28 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
         block_barrier();
         const int ahead = kt + NST - 1;
         if constexpr (SPREAD) {
-            compute(kt % NST, ahead < nk ? ahead % NST : -1, ahead * BK);
+            compute(kt % NST, ahead < nk ? ahead % NST : -1, (kt0 + ahead) * BK);
         } else {
-            if (ahead < nk) issue(ahead % NST, ahead * BK);
+            if (ahead < nk) issue(ahead % NST, (kt0 + ahead) * BK);
             compute(kt % NST, -1, 0);
         }
     }
 
+    if constexpr (BM <= 32 || NW == 8) {
+        // split K: the last split to finish a tile sums all partials in split
+        // order and alone runs the epilogue (one atomic per output element and
+        // pair, as without splits)
+        if (nsplit > 1 && !splitk_fixup<MB, NB, NW>(a, acc, tile, ks, nsplit, wave, lane)) return;
+    }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w);
 }
 
 template <int DT, int MODE>
 hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
-    const int nwg = a.m_tiles_max * a.n_tiles;
+    // one workgroup per (row tile, column tile, K split)
+    const long long nwg_l = (long long)a.m_tiles_max * a.n_tiles * (a.ksplit > 1 ? a.ksplit : 1);
+    if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
+    const int nwg = (int)nwg_l;
     if (nwg <= 0) return hipSuccess;
     if constexpr (DT == kF32) {
         return hipErrorInvalidValue;
@@ -355,6 +378,9 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
                 break;
             case kLds256k32s:
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 4, MODE, true>), dim3(nwg), dim3(256), 0, stream, a);
+                break;
+            case kLdsRows32:
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, false, 1>), dim3(nwg), dim3(256), 0, stream, a);
                 break;
             default:
                 return hipErrorInvalidValue;

@@ -129,7 +129,8 @@ int candle_moe_set_combine_policy(int policy);
  * LDS-DMA MFMA kernels 3 = 256x256 (BK 32), 4 = 256x128, 5 = 128x128,
  * 6 = 256x256 (BK 64, 4 waves), 7 = 256x256 (8 waves), 8 = 256x256 (8 waves,
  * BK 32), 9 = 256x256 (8 waves alternating MFMA and memory phases),
- * 10 / 11 = 256x256 BK 32 with the DMA spread over the K loop, 8 / 4 waves. */
+ * 10 / 11 = 256x256 BK 32 with the DMA spread over the K loop, 8 / 4 waves,
+ * 12 = 32x256 (chosen by default when experts get <= 32 rows on average). */
 int candle_moe_set_tile_policy(int policy);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
@@ -178,8 +179,9 @@ int candle_moe_apply_topk_softmax_inplace(const cm_tensor_t* gating_output, cons
 
 /* FusedMoE::forward (/root/reference/src/lib.rs:273-335). `output` is the
  * [num_tokens, hidden_dim] tensor of the input dtype that forward returns in
- * the reference; it is zeroed here (Tensor::zeros at lib.rs:296) before the
- * launch. down_weights may be NULL (Rust None). */
+ * the reference (Tensor::zeros at lib.rs:296 plus the accumulation): every
+ * element is written, so it needs no clearing. down_weights may be NULL
+ * (Rust None). */
 int candle_moe_fused_moe_forward(const cm_fused_moe_t* moe, const cm_tensor_t* input,
                                  const cm_tensor_t* gate_weights, const cm_tensor_t* up_weights,
                                  const cm_tensor_t* down_weights, const cm_tensor_t* routing_weights,

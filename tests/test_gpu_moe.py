@@ -246,7 +246,7 @@ def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32, 64, 256, 8, 2, O.F32) == "simt"
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("combine", [1, 2])
 def test_tile_configs(tile, combine):
     # both MFMA block tiles on both combine paths, ragged groups and column tails
