@@ -104,78 +104,113 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     const i32x4 rA = make_rsrc(a.A, a.a_bytes);
     const uint32_t smem_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
-    // ---- per-lane DMA sources. A: instruction i of this wave covers rows
-    // RPA*q .. RPA*q+RPA-1, q = NW*i + wave.
-    uint32_t a_row[A_INS];
-    int a_kc[A_INS];
+    // ---- per-lane DMA offsets, fixed for the whole K loop (gathered row or
+    // column chunk and the chunk's swizzled slot); the K position of a full
+    // tile goes into the instruction's SGPR offset. A: instruction i of this
+    // wave covers rows RPA*q .. RPA*q+RPA-1, q = NW*i + wave. Lanes outside the
+    // operand carry kOob (the buffer returns zeros).
+    uint32_t a_off[A_INS];
 #pragma unroll
     for (int i = 0; i < A_INS; ++i) {
         const int r = RPA * (NW * i + wave) + lane / ACH;
-        a_kc[i] = a_swz<ACH>(r, lane % ACH) * 8;  // k offset of the chunk that lands at this lane's slot
+        const int kc = a_swz<ACH>(r, lane % ACH) * 8;  // k offset of the chunk that lands at this lane's slot
+        a_off[i] = kOob;
         if (r < m_valid) {
             const int src = GATHER ? a.sorted_pair[r0 + r] / a.k_top : r0 + r;
-            a_row[i] = (uint32_t)src * (uint32_t)a_pitch * 2u;
-        } else {
-            a_row[i] = kOob;
+            a_off[i] = ((uint32_t)src * (uint32_t)a_pitch + (uint32_t)kc) * 2u;
         }
     }
-    // B: [K,N] sub-tiles: instruction i (i % SUB_INS within sub-tile i / SUB_INS)
-    // covers k-rows RPI*q .. RPI*q+RPI-1; [N,K] tiles: like A.
-    uint32_t b_col[B_INS];  // byte offset of the column chunk (or n-row start for [N,K])
-    int b_r[B_INS];         // k-row in tile ([K,N]) / k offset of the chunk ([N,K])
+    // B [N,K]: like A over the column tile's rows n. B [K,N]: instruction i
+    // (i % SUB_INS within sub-tile i / SUB_INS) covers k-rows RPI*q ..
+    // RPI*q+RPI-1 of the tile, q = NW*(i % SUB_INS) + wave.
+    uint32_t b_off[B_INS];
 #pragma unroll
     for (int i = 0; i < B_INS; ++i) {
         if constexpr (BNK) {
             const int r = RPA * (NW * i + wave) + lane / ACH;
             const int n = nt * BN + r;
-            b_r[i] = a_swz<ACH>(r, lane % ACH) * 8;
-            b_col[i] = n < N ? (uint32_t)n * (uint32_t)a.ldb * 2u : kOob;
+            const int kc = a_swz<ACH>(r, lane % ACH) * 8;
+            b_off[i] = n < N ? ((uint32_t)n * (uint32_t)a.ldb + (uint32_t)kc) * 2u : kOob;
         } else {
             const int q = NW * (i % SUB_INS) + wave;
             const int r = RPI * q + lane / BCH;
             const int c = kn_swz<BCH>(r, lane % BCH);
             const int col = nt * SUBN + c * 8;
-            b_r[i] = r;
-            b_col[i] = col < N ? (uint32_t)col * 2u : kOob;
+            b_off[i] = col < N ? ((uint32_t)col + (uint32_t)r * (uint32_t)a.ldb) * 2u : kOob;
         }
     }
+
+    // Weight buffer resources of the current expert; on the expert-set path
+    // the expert changes every seg_len of K (tracked as K advances, issue
+    // calls come in increasing k0).
+    int seg = 0, seg_k0 = 0;
+    auto weights_rsrc = [&](int e, i32x4& r0s, i32x4& r1s) {
+        const long long eoff = (long long)e * a.strideB;
+        r0s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B0) + eoff, a.strideB * 2);
+        r1s = r0s;
+        if constexpr (DUAL) r1s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B1) + eoff, a.strideB * 2);
+    };
+    i32x4 rB0, rB1;
+    weights_rsrc(seg_exp[0], rB0, rB1);
 
     // DMA instructions lo .. hi-1 of this wave's LOADS for the tile at k0
     // (A instructions first, then B).
     auto issue_range = [&](int stage, int k0, int lo, int hi) {
         const uint32_t sA = smem_base + stage * STAGE;
         const uint32_t sB = sA + A_BYTES;
-#pragma unroll
-        for (int i = 0; i < A_INS; ++i) {
-            if (i < lo || i >= hi) continue;
-            const int kc = k0 + a_kc[i];
-            const uint32_t off = (a_row[i] == kOob || kc >= K) ? kOob : a_row[i] + (uint32_t)kc * 2u;
-            dma16(rA, sA + (NW * i + wave) * 1024, off);
-        }
-        int kk = k0, klim = K, e = seg_exp[0];
+        int kk = k0, klim = K;
         if constexpr (SET) {
-            const int s = k0 / a.seg_len;
-            e = seg_exp[s < kSetMaxK ? s : 0];
-            kk = k0 - s * a.seg_len;
+            if (k0 >= seg_k0 + a.seg_len) {
+                while (k0 >= seg_k0 + a.seg_len) {
+                    ++seg;
+                    seg_k0 += a.seg_len;
+                }
+                weights_rsrc(seg_exp[seg < kSetMaxK ? seg : 0], rB0, rB1);
+            }
+            kk = k0 - seg_k0;
             klim = a.seg_len;
         }
-        const long long eoff = (long long)e * a.strideB;
-        const i32x4 r0s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B0) + eoff, a.strideB * 2);
-        i32x4 r1s = r0s;
-        if constexpr (DUAL) r1s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B1) + eoff, a.strideB * 2);
+        // a tile that lies inside the operands in K takes the SGPR-offset path;
+        // a K tail checks every lane's chunk against K
+        const uint32_t sa = (uint32_t)k0 * 2u;
+        const uint32_t sb = BNK ? (uint32_t)kk * 2u : (uint32_t)kk * (uint32_t)a.ldb * 2u;
+        if (k0 + BK <= K && kk + BK <= klim) {
+            // the tile lies inside the operands in K: one SGPR offset for all lanes
 #pragma unroll
-        for (int i = 0; i < B_INS; ++i) {
-            if (A_INS + i < lo || A_INS + i >= hi) continue;
-            uint32_t off;
-            if constexpr (BNK) {
-                const int kc = kk + b_r[i];
-                off = (b_col[i] == kOob || kc >= klim) ? kOob : b_col[i] + (uint32_t)kc * 2u;
-                dma16(r0s, sB + (NW * i + wave) * 1024, off);
-            } else {
-                const int kr = kk + b_r[i];
-                off = (b_col[i] == kOob || kr >= klim) ? kOob : b_col[i] + (uint32_t)kr * (uint32_t)a.ldb * 2u;
-                const int sub = i / SUB_INS;  // compile-time after unrolling
-                dma16(sub ? r1s : r0s, sB + sub * SUB_BYTES + (NW * (i % SUB_INS) + wave) * 1024, off);
+            for (int i = 0; i < A_INS; ++i)
+                if (i >= lo && i < hi) dma16s(rA, sA + (NW * i + wave) * 1024, a_off[i], sa);
+#pragma unroll
+            for (int i = 0; i < B_INS; ++i) {
+                if (A_INS + i < lo || A_INS + i >= hi) continue;
+                if constexpr (BNK) {
+                    dma16s(rB0, sB + (NW * i + wave) * 1024, b_off[i], sb);
+                } else {
+                    const int sub = i / SUB_INS;  // compile-time after unrolling
+                    dma16s(sub ? rB1 : rB0, sB + sub * SUB_BYTES + (NW * (i % SUB_INS) + wave) * 1024, b_off[i], sb);
+                }
+            }
+        } else {
+            // K tail: every lane's chunk is checked against the operand's K
+#pragma unroll
+            for (int i = 0; i < A_INS; ++i) {
+                if (i < lo || i >= hi) continue;
+                const int r = RPA * (NW * i + wave) + lane / ACH;
+                const bool in = k0 + a_swz<ACH>(r, lane % ACH) * 8 < K;
+                dma16s(rA, sA + (NW * i + wave) * 1024, in ? a_off[i] : kOob, sa);
+            }
+#pragma unroll
+            for (int i = 0; i < B_INS; ++i) {
+                if (A_INS + i < lo || A_INS + i >= hi) continue;
+                if constexpr (BNK) {
+                    const int r = RPA * (NW * i + wave) + lane / ACH;
+                    const bool in = kk + a_swz<ACH>(r, lane % ACH) * 8 < klim;
+                    dma16s(rB0, sB + (NW * i + wave) * 1024, in ? b_off[i] : kOob, sb);
+                } else {
+                    const int sub = i / SUB_INS;
+                    const bool in = kk + RPI * (NW * (i % SUB_INS) + wave) + lane / BCH < klim;
+                    dma16s(sub ? rB1 : rB0, sB + sub * SUB_BYTES + (NW * (i % SUB_INS) + wave) * 1024,
+                           in ? b_off[i] : kOob, sb);
+                }
             }
         }
     };
