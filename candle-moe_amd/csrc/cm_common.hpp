@@ -136,6 +136,29 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 }
 
 __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Workgroup -> logical work item. The hardware hands workgroup w to XCD w % 8;
+// this gives each XCD a contiguous range of the `live` items (neighbouring
+// tiles then share that XCD's L2) and spreads the live items evenly over the
+// 8 XCDs, however many spare workgroups a grid sized for the worst case holds.
+// Returns -1 for a workgroup with no item.
+__device__ __forceinline__ int xcd_logical(int live) {
+    live = min(live, (int)gridDim.x);
+    const int w = blockIdx.x, xcd = w & 7, idx = w >> 3;
+    const int per = live >> 3, rem = live & 7;
+    if (idx >= per + (xcd < rem ? 1 : 0)) return -1;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Output tile (row tile mt, column tile nt) of this workgroup, or false when
+// it has none: the row-tile count m_live comes from the grouping on the device.
+__device__ __forceinline__ bool tile_coords(int n_tiles, int m_live, int& mt, int& nt) {
+    const int logical = xcd_logical(m_live * n_tiles);
+    if (logical < 0) return false;
+    mt = logical / n_tiles;
+    nt = logical - mt * n_tiles;
+    return true;
+}
 __host__ __device__ __forceinline__ long long cdivll(long long a, long long b) { return (a + b - 1) / b; }
 
 }  // namespace cm

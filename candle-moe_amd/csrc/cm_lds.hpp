@@ -80,19 +80,6 @@ __device__ __forceinline__ int kn_swz(int r, int c) {
     else return c ^ (((r >> 1) & 1) << 2);
 }
 
-// Bijective remap of the hardware dispatch order (workgroup w runs on XCD
-// w % 8) to a logical id that is contiguous per XCD.
-__device__ __forceinline__ int logical_wg() {
-    const int nwg = gridDim.x;
-    const int w = blockIdx.x;
-    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
-    return xcd * per + (xcd < rem ? xcd : rem) + idx;
-}
-__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
-    const int logical = logical_wg();
-    mt = logical / n_tiles;
-    nt = logical - mt * n_tiles;
-}
 
 // Clear this workgroup's share of n floats at p (16-byte stores where p is
 // 16-byte aligned, which the workspace guarantees).

@@ -45,17 +45,6 @@ constexpr int kBK = 64;  // K elements per LDS stage
 
 __device__ __forceinline__ int swz(int row, int c) { return row * 128 + (((c ^ row ^ (row >> 3)) & 7) << 4); }
 
-// Bijective remap of the hardware dispatch order (workgroup w runs on XCD
-// w % 8) to a logical tile id that is contiguous per XCD.
-__device__ __forceinline__ void tile_coords(int n_tiles, int& mt, int& nt) {
-    const int nwg = gridDim.x;
-    const int w = blockIdx.x;
-    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, idx = w >> 3;
-    const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
-    mt = logical / n_tiles;
-    nt = logical - mt * n_tiles;
-}
-
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
@@ -81,8 +70,7 @@ __global__ __launch_bounds__(256, 1) void moe_mfma_gemm(GemmArgs a) {
     __shared__ float s_w[ATOMIC ? BM : 1];
 
     int mt, nt;
-    tile_coords(a.n_tiles, mt, nt);
-    if (mt >= *a.num_tiles) return;
+    if (!tile_coords(a.n_tiles, *a.num_tiles, mt, nt)) return;
     const int r0 = a.tile_row[mt];
     const int grp = a.tile_exp[mt];  // expert, or expert-set key
     const int m_valid = min(BM, a.offsets[grp + 1] - r0);
@@ -374,8 +362,7 @@ __global__ __launch_bounds__(256) void moe_simt_gemm(GemmArgs a) {
     __shared__ long long s_row[TM];
 
     int mt, nt;
-    tile_coords(a.n_tiles, mt, nt);
-    if (mt >= *a.num_tiles) return;
+    if (!tile_coords(a.n_tiles, *a.num_tiles, mt, nt)) return;
     const int r0 = a.tile_row[mt];
     const int e = a.tile_exp[mt];
     const int m_valid = min(TM, a.offsets[e + 1] - r0);

@@ -79,10 +79,10 @@ __global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
     // share of zero_f32 (the accumulator of the GEMM that follows)
     clear_share(a.zero_f32, a.zero_n);
     const int nsplit = a.ksplit > 1 ? a.ksplit : 1;
-    const int lg = logical_wg();
+    const int lg = xcd_logical(*a.num_tiles * a.n_tiles * nsplit);
+    if (lg < 0) return;
     const int tile = lg / nsplit, ks = lg - tile * nsplit;
     const int mt = tile / a.n_tiles, nt = tile - mt * a.n_tiles;
-    if (mt >= *a.num_tiles) return;
     const int r0 = a.tile_row[mt];
     const int grp = a.tile_exp[mt];
     const int m_valid = min(BM, a.offsets[grp + 1] - r0);

@@ -74,8 +74,7 @@ __global__ __launch_bounds__(512, 1) void moe_pp_gemm(GemmArgs a) {
     __shared__ float s_w[ATOMIC ? BM : 1];
 
     int mt, nt;
-    tile_coords(a.n_tiles, mt, nt);
-    if (mt >= *a.num_tiles) return;
+    if (!tile_coords(a.n_tiles, *a.num_tiles, mt, nt)) return;
     const int r0 = a.tile_row[mt];
     const int ge = a.tile_exp[mt];  // expert (pair grouping) or expert-set key
     const int m_valid = min(BM, a.offsets[ge + 1] - r0);
