@@ -195,15 +195,23 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.T = T; p.H = H; p.I = I; p.E = E; p.k = k; p.act = act; p.moe_type = (int)moe_type; p.dtype = (int)dtype;
     p.P = P;
     p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
-    // Default MFMA kernel: LDS-DMA, 256x256 block tile, 8 waves (measured
-    // fastest on every BASELINE shape from a few hundred rows per expert up,
-    // including the skewed E=128 one). With at most 32 rows per touched expert
-    // on average (decode) the GEMMs stream each touched expert's weights once
-    // and the 32-row tile keeps the padding and the MFMA work small.
+    // Default MFMA kernel, by rows per touched expert (measured on MI355X
+    // over T = 1 .. 32768 of the Qwen3, Qwen3-30B and Nomic shapes):
+    //  * at most 32 (decode): the GEMMs stream each touched expert's weights
+    //    once; the 32-row tile keeps the padding and the MFMA work small;
+    //  * at most 128, where the 256x256 tile would leave fewer than 256
+    //    workgroups (few experts): the 128x128 tile, which doubles to
+    //    quadruples the workgroups;
+    //  * otherwise the 256x256 tile with 8 waves.
+    // Expected live row tiles of a tile height: one per touched expert at
+    // least, the rows over the tile height at least.
+    const long long touched = P < E ? P : E;
+    auto est_tiles = [&](int bm) { return std::max<long long>((P + bm - 1) / bm, touched); };
     p.cfg = !p.mfma ? kTileSimt : (g_tile_policy ? g_tile_policy : kLds256w8);
     if (p.mfma && !g_tile_policy) {
-        const long long touched = P < E ? P : E;
+        const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
+        else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
     }
     // the LDS-DMA kernels address operands with 32-bit buffer offsets
     if (is_lds_cfg(p.cfg)) {
@@ -228,20 +236,20 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= 0.5 * p.BM * sets);
         }
     }
-    // K splits for the 32-row (decode) GEMMs whose output tiles leave most
-    // CUs idle (< 64 tiles): up to ~256 workgroups, at most 8 splits, no empty
-    // split. Each split writes a 32 KB f32 partial that the last one sums, so
-    // splitting only pays where the weight stream would otherwise run on a
-    // few CUs.
+    // K splits for the 32-row (decode) GEMMs whose expected output tiles
+    // (< 128) leave most CUs idle: up to ~256 workgroups, at most 8 splits,
+    // no empty split. Each split writes a 32 KB f32 partial that the last one
+    // sums, so splitting only pays where the weight stream would otherwise run
+    // on a few CUs.
     p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
     p.split1 = p.split2 = 1;
     if (p.lds_family && p.cfg == kLdsRows32 && P > 0) {
-        const long long mt = grouping_max_tiles(P, E, p.BM);
+        const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);
         auto choose = [&](long long tiles, int K) {
-            if (tiles >= 64) return 1;
+            if (tiles >= 128) return 1;
             const int nk = (K + bk - 1) / bk;
             long long sp = (256 + tiles - 1) / tiles;
             if (sp > 8) sp = 8;

@@ -25,7 +25,8 @@ struct GroupingBufs {
     int32_t* zero_ptr;      // ints cleared before the GEMMs run (may be null)
     int zero_n;
 };
-constexpr int kGroupChunk = 4096;  // pairs per grouping workgroup
+constexpr int kGroupChunk = 1024;      // items per workgroup of the multi-workgroup grouping
+constexpr int kGroupSmallMax = 4096;   // up to this many items: one-workgroup grouping
 inline int grouping_blocks(long long P) { return (int)((P + kGroupChunk - 1) / kGroupChunk); }
 // Row tiles of a grouping: sum over non-empty groups of ceil(count / BM)
 // <= ceil(P / BM) + (number of non-empty groups).

@@ -9,12 +9,16 @@
 // deterministic), and the multi-block path scans per-block counts instead of
 // aliasing counts and offsets (/root/reference/kernels/preprocessing.cuh:296-298).
 //
-// Three launches, all multi-workgroup, no host synchronisation:
-//   1. grouping_hist   : each workgroup histograms kGroupChunk pairs in LDS
+// Up to kGroupSmallMax items one workgroup does everything (grouping_small).
+// Beyond that, three launches, no host synchronisation:
+//   1. grouping_hist   : each workgroup histograms kGroupChunk items in LDS
 //   2. grouping_scan   : one workgroup turns the per-block counts into
-//                        per-block bases, expert offsets and the tile table
-//   3. grouping_scatter: each workgroup re-reads its chunk and ranks pairs
-//                        stably with wave ballots (64-lane peer masks)
+//                        per-block bases (one wave-wide scan per bin), the bin
+//                        offsets and the tile table
+//   3. grouping_scatter: each workgroup re-reads its chunk and ranks items
+//                        stably: 64-lane peer masks from ballots inside a wave,
+//                        per-wave running counts in LDS, one barrier to turn
+//                        the per-wave counts into bases
 // The same three kernels group tokens by their expert set (TOK = true) for
 // the expert-set down projection.
 #include "cm_common.hpp"
@@ -84,108 +88,6 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_hist(const uint32_t* _
             s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
 }
 
-// One workgroup. block_counts[b][e] becomes the number of expert-e pairs in
-// blocks < b (its base inside the expert's segment).
-__global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int E, int BM,
-                                                               int32_t* __restrict__ block_counts,
-                                                               int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ tile_row,
-                                                               int32_t* __restrict__ tile_exp,
-                                                               int32_t* __restrict__ num_tiles) {
-    extern __shared__ int32_t s_tot[];  // [E] totals, then [E] tile bases
-    int32_t* s_tb = s_tot + E;
-    for (int e = threadIdx.x; e < E; e += kGroupThreads) {
-        int32_t run = 0;
-        for (int b = 0; b < nblocks; ++b) {
-            const long long o = (long long)b * E + e;
-            const int32_t c = block_counts[o];
-            block_counts[o] = run;
-            run += c;
-        }
-        s_tot[e] = run;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t sum = 0, mx = 0, tiles = 0;
-        for (int e = 0; e < E; ++e) {
-            const int32_t c = s_tot[e];
-            offsets[e] = sum;
-            s_tb[e] = tiles;
-            mx = c > mx ? c : mx;
-            sum += c;
-            tiles += (c + BM - 1) / BM;
-        }
-        offsets[E] = sum;
-        offsets[E + 1] = mx;
-        *num_tiles = tiles;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += kGroupThreads) {
-        const int32_t c = s_tot[e];
-        const int32_t nt = (c + BM - 1) / BM;
-        const int32_t o = offsets[e];
-        const int32_t tb = s_tb[e];
-        for (int i = 0; i < nt; ++i) {
-            tile_row[tb + i] = o + i * BM;
-            tile_exp[tb + i] = e;
-        }
-    }
-}
-
-template <bool TOK>
-__global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t* __restrict__ idx, long long P,
-                                                                  int k, int E, int nbins, int ebits,
-                                                                  const int32_t* __restrict__ block_counts,
-                                                                  const int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ sorted_pair,
-                                                                  int32_t* __restrict__ pair_dest) {
-    extern __shared__ int32_t s_mem[];
-    const int E_ = nbins;
-    int32_t* s_run = s_mem;           // [bins] next free position per bin
-    int32_t* s_wc = s_mem + E_;       // [4][bins] per-wave counts of the current step
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    for (int e = threadIdx.x; e < E_; e += kGroupThreads) {
-        s_run[e] = offsets[e] + block_counts[(long long)blockIdx.x * E_ + e];
-        s_wc[e] = s_wc[E_ + e] = s_wc[2 * E_ + e] = s_wc[3 * E_ + e] = 0;
-    }
-    __syncthreads();
-    const long long base = (long long)blockIdx.x * kGroupChunk;
-    const long long end = base + kGroupChunk < P ? base + kGroupChunk : P;
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (long long s = base; s < end; s += kGroupThreads) {
-        const long long p = s + threadIdx.x;
-        int rank[kSetMaxK];
-        const int bin = p < end ? item_bin<TOK>(idx, p, k, E, rank) : -1;
-        const bool active = bin >= 0;
-        const uint32_t e = active ? (uint32_t)bin : 0xffffffffu;
-        // Lanes of this wave holding the same expert: AND of per-bit ballots.
-        uint64_t peers = __ballot(active);
-        for (int b = 0; b < ebits; ++b) {
-            const bool bit = (e >> b) & 1u;
-            const uint64_t bal = __ballot(bit);
-            peers &= bit ? bal : ~bal;
-        }
-        const int lrank = __popcll(peers & lt_mask);
-        if (active && lrank == 0) s_wc[wave * E_ + e] = __popcll(peers);
-        __syncthreads();
-        if (active) {
-            int32_t pos = s_run[e] + lrank;
-            for (int w = 0; w < wave; ++w) pos += s_wc[w * E_ + e];
-            sorted_pair[pos] = (int32_t)p;
-            if constexpr (TOK) {
-                for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
-            }
-        }
-        __syncthreads();
-        for (int ee = threadIdx.x; ee < E_; ee += kGroupThreads) {
-            s_run[ee] += s_wc[ee] + s_wc[E_ + ee] + s_wc[2 * E_ + ee] + s_wc[3 * E_ + ee];
-            s_wc[ee] = s_wc[E_ + ee] = s_wc[2 * E_ + ee] = s_wc[3 * E_ + ee] = 0;
-        }
-        __syncthreads();
-    }
-}
-
 // Exclusive scan of v[0..n) in place (one workgroup of kGroupThreads),
 // returning the total; s_part is kGroupThreads ints of scratch. Each thread
 // scans a contiguous run of ceil(n / threads) entries.
@@ -215,7 +117,131 @@ __device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
     return total;
 }
 
-// All of grouping in one workgroup, for at most kGroupChunk items: LDS
+// One workgroup. block_counts[b][e] becomes the number of bin-e items in
+// blocks < b (its base inside the bin's segment): bins go round-robin to the
+// waves, each scans its bin over the blocks 64 at a time. Then the bin totals
+// and tile counts are scanned into offsets and the tile table.
+__global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int nbins, int BM,
+                                                               int32_t* __restrict__ block_counts,
+                                                               int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ tile_row,
+                                                               int32_t* __restrict__ tile_exp,
+                                                               int32_t* __restrict__ num_tiles) {
+    extern __shared__ int32_t s_tot[];  // [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads]
+    int32_t* s_tb = s_tot + nbins;
+    int32_t* s_part = s_tb + nbins;
+    __shared__ int32_t s_max;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (threadIdx.x == 0) s_max = 0;
+    for (int e = wave; e < nbins; e += kGroupThreads / 64) {
+        int32_t carry = 0;
+        for (int b0 = 0; b0 < nblocks; b0 += 64) {
+            const int b = b0 + lane;
+            const long long o = (long long)b * nbins + e;
+            const int32_t c = b < nblocks ? block_counts[o] : 0;
+            int32_t incl = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int32_t t = __shfl_up(incl, d);
+                if (lane >= d) incl += t;
+            }
+            if (b < nblocks) block_counts[o] = carry + incl - c;
+            carry += __shfl(incl, 63);
+        }
+        if (lane == 0) {
+            s_tot[e] = carry;
+            s_tb[e] = (carry + BM - 1) / BM;
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) atomicMax(&s_max, s_tot[e]);
+    const int32_t total = block_exclusive_scan(s_tot, nbins, s_part);
+    const int32_t tiles = block_exclusive_scan(s_tb, nbins, s_part);
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+        offsets[e] = s_tot[e];
+        const int32_t c = (e + 1 < nbins ? s_tot[e + 1] : total) - s_tot[e];
+        const int32_t nt = (c + BM - 1) / BM;
+        for (int i = 0; i < nt; ++i) {
+            tile_row[s_tb[e] + i] = s_tot[e] + i * BM;
+            tile_exp[s_tb[e] + i] = e;
+        }
+    }
+    if (threadIdx.x == 0) {
+        offsets[nbins] = total;
+        offsets[nbins + 1] = s_max;
+        *num_tiles = tiles;
+    }
+}
+
+// Stable scatter of one kGroupChunk block. Wave w ranks items
+// [w*64*IPT, (w+1)*64*IPT) of the block, 64 at a time: lanes holding the same
+// bin find each other with ballots over the bin's bits, and a per-wave LDS
+// count per bin carries the rank from one step to the next. After one barrier
+// the per-wave counts become per-wave bases (block base of the bin + counts
+// of the waves before), and every item goes to base + its rank.
+template <bool TOK>
+__global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t* __restrict__ idx, long long P,
+                                                                  int k, int E, int nbins, int ebits,
+                                                                  const int32_t* __restrict__ block_counts,
+                                                                  const int32_t* __restrict__ offsets,
+                                                                  int32_t* __restrict__ sorted_pair,
+                                                                  int32_t* __restrict__ pair_dest) {
+    constexpr int NW = kGroupThreads / 64;
+    constexpr int IPT = kGroupChunk / kGroupThreads;  // items per lane
+    extern __shared__ int32_t s_wc[];                  // [NW][nbins] per-wave counts, then bases
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_wc[i] = 0;
+    __syncthreads();
+    int32_t* mine = s_wc + wave * nbins;
+    const long long wbase = (long long)blockIdx.x * kGroupChunk + wave * 64 * IPT;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int bin[IPT], lrank[IPT];
+    int rank[kSetMaxK];
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        const long long p = wbase + s * 64 + lane;
+        const int b = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        const bool active = b >= 0;
+        const uint32_t e = active ? (uint32_t)b : 0xffffffffu;
+        uint64_t peers = __ballot(active);
+        for (int i = 0; i < ebits; ++i) {
+            const bool bit = (e >> i) & 1u;
+            const uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        const int r = __popcll(peers & lt_mask);
+        // every lane reads the running count before the bin's first lane
+        // stores the new one (LDS instructions of a wave execute in order)
+        const int before = active ? mine[b] : 0;
+        if (active && r == 0) mine[b] = before + __popcll(peers);
+        bin[s] = b;
+        lrank[s] = before + r;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+        int32_t run = offsets[e] + block_counts[(long long)blockIdx.x * nbins + e];
+        for (int w = 0; w < NW; ++w) {
+            const int32_t c = s_wc[w * nbins + e];
+            s_wc[w * nbins + e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        if (bin[s] < 0) continue;
+        const long long p = wbase + s * 64 + lane;
+        const int32_t pos = mine[bin[s]] + lrank[s];
+        sorted_pair[pos] = (int32_t)p;
+        if constexpr (TOK) {
+            (void)token_set_key(idx, p, k, E, rank);
+            for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
+        }
+    }
+}
+
+// All of grouping in one workgroup, for at most kGroupSmallMax items: LDS
 // histogram, block-wide scans of the counts and of the per-bin tile counts,
 // the tile table, and the stable ballot scatter. Also clears zero_n ints at
 // zero_ptr (the split-K arrival counters of the GEMMs that follow).
@@ -310,7 +336,7 @@ static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int
     int bbits0 = 0;
     while ((1 << bbits0) < nbins) ++bbits0;
     // LDS of the one-workgroup path: 6 * nbins + threads ints
-    if (items <= kGroupChunk && (6LL * nbins + kGroupThreads) * 4 <= 64 * 1024) {
+    if (items <= kGroupSmallMax && (6LL * nbins + kGroupThreads) * 4 <= 64 * 1024) {
         hipLaunchKernelGGL((grouping_small<TOK>), dim3(1), dim3(kGroupThreads),
                            (6 * nbins + kGroupThreads) * sizeof(int32_t), stream, idx, (int)items, k, E, nbins, bbits0,
                            BM, b.offsets, b.sorted_pair, b.tile_row, b.tile_exp, b.num_tiles, pair_dest, b.zero_ptr,
@@ -328,10 +354,10 @@ static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int
         hipLaunchKernelGGL((grouping_hist<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t), stream,
                            idx, items, k, E, nbins, b.block_counts);
     }
-    hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), 2 * nbins * sizeof(int32_t), stream, nb, nbins,
-                       BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles);
+    hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), (2 * nbins + kGroupThreads) * sizeof(int32_t),
+                       stream, nb, nbins, BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles);
     if (nb > 0) {
-        hipLaunchKernelGGL((grouping_scatter<TOK>), dim3(nb), dim3(kGroupThreads), 5 * nbins * sizeof(int32_t),
+        hipLaunchKernelGGL((grouping_scatter<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t),
                            stream, idx, items, k, E, nbins, bbits, b.block_counts, b.offsets, b.sorted_pair,
                            pair_dest);
     }

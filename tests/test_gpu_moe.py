@@ -240,6 +240,27 @@ def test_expert_set_path_dropped_and_repeated_experts():
     assert (got[2::11] == 0).all()
 
 
+def test_multi_block_grouping_skewed_dropped_repeated():
+    # more items than the one-workgroup grouping takes (per-block histograms,
+    # the cross-block scan, the block scatter), with a skewed load, dropped
+    # ids and repeated experts, every row checked on both combine paths
+    T, H, I, E, k = 9000, 64, 64, 8, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 31, O.QWEN3)
+    ri = ri.copy()
+    ri[::2, 0] = 3
+    ri[::13, 1] = 50
+    ri[5::17, 1] = ri[5::17, 0]
+    kw = dict(E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16)
+    want = O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_F32ACC, **kw)
+    for combine in (candle_moe.COMBINE_PAIRS, candle_moe.COMBINE_EXPERT_SETS):
+        try:
+            candle_moe.set_combine_policy(combine)
+            got = run_moe(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16)
+        finally:
+            candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+        assert_close(got, want, RTOL[O.BF16], "combine %d" % combine)
+
+
 def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32768, 4096, 1536, 8, 2, O.BF16) == "expert-set"
     assert candle_moe.fused_moe_path(4096, 2048, 768, 128, 8, O.BF16) == "pairs"
