@@ -114,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_profile_end.restype = i32
         L.candle_moe_profile_slot_name.argtypes = [i32]
         L.candle_moe_profile_slot_name.restype = ctypes.c_char_p
+        L.candle_moe_trim_workspaces.argtypes = []
+        L.candle_moe_trim_workspaces.restype = i32
         L.candle_moe_last_error.argtypes = []
         L.candle_moe_last_error.restype = ctypes.c_char_p
         L.candle_moe_version.argtypes = []
@@ -268,6 +270,12 @@ class FusedMoE:
             int(moe_type), ctypes.byref(output)))
 
 
+def trim_workspaces() -> None:
+    """Release the library-owned fused_moe workspaces (one per device and
+    stream, kept between calls); the next call allocates again."""
+    check(lib().candle_moe_trim_workspaces())
+
+
 def version() -> str:
     return lib().candle_moe_version().decode()
 
@@ -282,8 +290,9 @@ def set_combine_policy(policy: int) -> None:
 
 
 (TILE_AUTO, TILE_128, TILE_256, TILE_LDS_256, TILE_LDS_256x128, TILE_LDS_128, TILE_LDS_256K64, TILE_W8, TILE_W8K32,
- TILE_PINGPONG, TILE_W8K32_SPREAD, TILE_K32_SPREAD, TILE_ROWS32) = range(13)
-_TILE_ROWS = {0: 64, 1: 128, 2: 256, 3: 256, 4: 256, 5: 128, 6: 256, 7: 256, 8: 256, 9: 256, 10: 256, 11: 256, 12: 32}
+ TILE_PINGPONG, TILE_W8K32_SPREAD, TILE_K32_SPREAD, TILE_ROWS32, TILE_256x128_OCC2, TILE_128x256_OCC2) = range(15)
+_TILE_ROWS = {0: 64, 1: 128, 2: 256, 3: 256, 4: 256, 5: 128, 6: 256, 7: 256, 8: 256, 9: 256, 10: 256, 11: 256, 12: 32,
+              13: 256, 14: 128}
 
 
 def set_tile_policy(policy: int) -> None:

@@ -58,6 +58,16 @@ struct ProfRec {
 static std::mutex g_prof_mu;
 static bool g_prof_on = false;
 static std::vector<ProfRec> g_prof;
+static std::vector<hipEvent_t> g_event_pool;  // events of finished sessions, reused (creation costs host time)
+
+static bool pooled_event_locked(hipEvent_t& ev) {
+    if (!g_event_pool.empty()) {
+        ev = g_event_pool.back();
+        g_event_pool.pop_back();
+        return true;
+    }
+    return hipEventCreate(&ev) == hipSuccess;
+}
 
 struct ProfScope {
     ProfRec rec;
@@ -67,9 +77,16 @@ struct ProfScope {
         std::lock_guard<std::mutex> lk(g_prof_mu);
         if (!g_prof_on) return;
         rec.slot = slot;
-        if (hipEventCreate(&rec.a) != hipSuccess) return;
-        if (hipEventCreate(&rec.b) != hipSuccess) { (void)hipEventDestroy(rec.a); return; }
+        if (!pooled_event_locked(rec.a)) return;
+        if (!pooled_event_locked(rec.b)) {
+            g_event_pool.push_back(rec.a);
+            return;
+        }
         on = hipEventRecord(rec.a, s) == hipSuccess;
+        if (!on) {
+            g_event_pool.push_back(rec.a);
+            g_event_pool.push_back(rec.b);
+        }
     }
     ~ProfScope() {
         if (!on) return;
@@ -202,6 +219,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     //  * at most 128, where the 256x256 tile would leave fewer than 256
     //    workgroups (few experts): the 128x128 tile, which doubles to
     //    quadruples the workgroups;
+    //  * at most 1024 with a hidden size of at most 2048 (short K loops of
+    //    the gate/up GEMM): the 128x256 tile, two workgroups per CU, so that
+    //    one's prologue, barriers and epilogue overlap the other's MFMAs;
     //  * otherwise the 256x256 tile with 8 waves.
     // Expected live row tiles of a tile height: one per touched expert at
     // least, the rows over the tile height at least.
@@ -212,6 +232,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
+        else if (H <= 2048 && P <= 1024 * touched) p.cfg = kLds128x256o2;
     }
     // the LDS-DMA kernels address operands with 32-bit buffer offsets
     if (is_lds_cfg(p.cfg)) {
@@ -431,19 +452,60 @@ static int check_ptrs(const Problem& p, const void* x, const void* gate, const v
 
 // Stream-ordered pool allocation; the pool keeps freed memory (release
 // threshold raised once per device) so repeated calls do not go to the driver.
-static void prepare_pool_once() {
-    static std::mutex mu;
-    static bool done[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
-    std::lock_guard<std::mutex> lk(mu);
-    if (done[dev]) return;
-    done[dev] = true;
-    hipMemPool_t pool;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-        uint64_t thr = ~0ull;
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &thr);
+// Library-owned workspaces, one per (device, stream), kept between calls and
+// grown when a call needs more: allocating and freeing a stream-ordered
+// workspace on every call costs ~50 us of host time, more than a whole
+// decode step's kernels. Reuse is safe because every call on a stream is
+// ordered after the previous one on that stream; the lock is held while a
+// call enqueues its kernels, so two host threads on one stream never
+// interleave their launches over the shared buffer. A grown buffer's old
+// allocation is released with hipFreeAsync on its own stream.
+struct OwnedWs {
+    int device;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+};
+static std::mutex g_ws_mu;
+static std::vector<OwnedWs> g_ws;
+
+static OwnedWs* owned_ws_locked(int dev, hipStream_t s, size_t need, hipError_t& err) {
+    err = hipSuccess;
+    OwnedWs* w = nullptr;
+    for (auto& e : g_ws)
+        if (e.device == dev && e.stream == s) w = &e;
+    if (w && w->bytes >= need) return w;
+    // grow by at least 1.5x and to whole MiB, so that a slowly growing T
+    // does not reallocate on every call
+    size_t want = need + need / 2;
+    want = (want + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    void* mem = nullptr;
+    err = hipMallocAsync(&mem, want, s);
+    if (err != hipSuccess) return nullptr;
+    if (w) {
+        if (w->ptr) (void)hipFreeAsync(w->ptr, s);
+        w->ptr = mem;
+        w->bytes = want;
+        return w;
     }
+    g_ws.push_back(OwnedWs{dev, s, mem, want});
+    return &g_ws.back();
+}
+
+int trim_owned_workspaces() {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) cur = -1;
+    hipError_t first = hipSuccess;
+    for (auto& e : g_ws) {
+        if (!e.ptr) continue;
+        if (e.device != cur) (void)hipSetDevice(e.device);
+        const hipError_t r = hipFreeAsync(e.ptr, e.stream);
+        if (first == hipSuccess) first = r;
+        if (e.device != cur && cur >= 0) (void)hipSetDevice(cur);
+    }
+    g_ws.clear();
+    return first == hipSuccess ? CANDLE_MOE_OK : hip_fail(first, "trim workspaces: hipFreeAsync");
 }
 
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
@@ -467,16 +529,15 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
         return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw),
                        reinterpret_cast<const uint32_t*>(idx), out, overwrite, reinterpret_cast<char*>(ws), s);
     }
-    prepare_pool_once();
-    void* mem = nullptr;
-    hipError_t e = hipMallocAsync(&mem, L.total, s);
-    if (e != hipSuccess) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s",
-                                          L.total, hipGetErrorString(e));
-    rc = run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                 out, overwrite, reinterpret_cast<char*>(mem), s);
-    e = hipFreeAsync(mem, s);
-    if (rc == CANDLE_MOE_OK && e != hipSuccess) return hip_fail(e, "fused_moe: hipFreeAsync");
-    return rc;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe: hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    OwnedWs* w = owned_ws_locked(dev, s, L.total, e);
+    if (!w) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s", L.total,
+                             hipGetErrorString(e));
+    return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
+                   out, overwrite, reinterpret_cast<char*>(w->ptr), s);
 }
 
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
@@ -546,6 +607,11 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
                               activation_type, moe_type, dtype, workspace, workspace_bytes, false, false, stream);
 }
 
+int candle_moe_trim_workspaces(void) {
+    cm::clear_error();
+    return cm::trim_owned_workspaces();
+}
+
 const char* candle_moe_last_error(void) { return cm::g_last_error.c_str(); }
 
 int candle_moe_set_combine_policy(int policy) {
@@ -595,8 +661,11 @@ int candle_moe_profile_end(double* total_ms, int* counts, int nslots) {
             if (total_ms) total_ms[r.slot] += ms;
             if (counts) counts[r.slot] += 1;
         }
-        (void)hipEventDestroy(r.a);
-        (void)hipEventDestroy(r.b);
+    }
+    std::lock_guard<std::mutex> lk(cm::g_prof_mu);
+    for (auto& r : recs) {
+        cm::g_event_pool.push_back(r.a);
+        cm::g_event_pool.push_back(r.b);
     }
     return rc;
 }

@@ -104,20 +104,26 @@ struct GemmArgs {
 // 4 stages: few rows per expert (decode), bound by streaming the weights.
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
-    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11, kLdsRows32 = 12
+    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11, kLdsRows32 = 12,
+    kLds256x128o2 = 13, kLds128x256o2 = 14
 };
-constexpr int kNumTileCfgs = 13;
+constexpr int kNumTileCfgs = 15;
 inline int tile_rows(int cfg) {
     if (cfg == kLdsRows32) return 32;
-    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128) ? 128 : 256);
+    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds128x256o2) ? 128 : 256);
 }
 inline int tile_cols(int cfg) {
-    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128) ? 128 : 256);
+    return (cfg == kTileSimt) ? 64
+                              : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128 || cfg == kLds256x128o2) ? 128
+                                                                                                                    : 256);
 }
 inline bool is_lds_cfg(int cfg) { return cfg >= kLds256; }
 // K tile of the LDS-DMA kernels
 inline int tile_bk(int cfg) {
-    return (cfg == kLds256 || cfg == kLds256w8k32 || cfg == kLds256w8k32s || cfg == kLds256k32s) ? 32 : 64;
+    return (cfg == kLds256 || cfg == kLds256w8k32 || cfg == kLds256w8k32s || cfg == kLds256k32s ||
+            cfg == kLds256x128o2 || cfg == kLds128x256o2)
+               ? 32
+               : 64;
 }
 
 bool mfma_supported(int dtype, int K, int N);

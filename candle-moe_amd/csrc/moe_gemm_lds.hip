@@ -29,8 +29,8 @@ namespace cm {
 
 using namespace lds;
 
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false, int WGM = 2>
-__global__ __launch_bounds__(64 * NW, 1) void moe_lds_gemm(GemmArgs a) {
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false, int WGM = 2, int OCC = 1>
+__global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // NW waves in WGM rows: 4 in a 2x2 layout (one per SIMD), 8 in 2x4 (two
     // per SIMD, so one wave's MFMAs cover the other's LDS, DMA and VALU work),
     // or all side by side along N (WGM = 1) for 32-row tiles, where the
@@ -416,6 +416,16 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
                 break;
             case kLdsRows32:
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, false, 1>), dim3(nwg), dim3(256), 0, stream, a);
+                break;
+            // two workgroups per CU (72 KB of LDS, at most 256 VGPRs each): one
+            // workgroup's barrier and DMA issue overlap the other's MFMAs
+            case kLds256x128o2:
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 128, 32, 3, 4, MODE, false, 2, 2>), dim3(nwg), dim3(256), 0,
+                                   stream, a);
+                break;
+            case kLds128x256o2:
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 256, 32, 3, 4, MODE, false, 2, 2>), dim3(nwg), dim3(256), 0,
+                                   stream, a);
                 break;
             default:
                 return hipErrorInvalidValue;

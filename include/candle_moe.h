@@ -65,8 +65,10 @@ void topk_softmax(const void* gating_output, void* topk_weight, void* topk_indic
  *   output         [num_tokens, hidden_dim]                       dtype, zero-initialised by
  *                                                                 the caller (results are added)
  * Qwen3: y = (act(x G) * (x U)) D.   Nomic: y = act(x G) U^T.
- * The workspace is taken from the device's stream-ordered memory pool
- * (hipMallocAsync / hipFreeAsync on `stream`); no host synchronisation.
+ * The workspace is library-owned: one buffer per (device, stream), allocated
+ * stream-ordered (hipMallocAsync on `stream`) on first use, grown when a call
+ * needs more and kept for the next call on that stream;
+ * candle_moe_trim_workspaces releases them. No host synchronisation.
  */
 void fused_moe(const void* input, const void* gate_weights, const void* up_weights,
                const void* down_weights, const void* routing_weights, const void* expert_indices,
@@ -130,13 +132,22 @@ int candle_moe_set_combine_policy(int policy);
  * 6 = 256x256 (BK 64, 4 waves), 7 = 256x256 (8 waves), 8 = 256x256 (8 waves,
  * BK 32), 9 = 256x256 (8 waves alternating MFMA and memory phases),
  * 10 / 11 = 256x256 BK 32 with the DMA spread over the K loop, 8 / 4 waves,
- * 12 = 32x256 (chosen by default when experts get <= 32 rows on average). */
+ * 12 = 32x256 (default when experts get <= 32 rows on average),
+ * 13 / 14 = 256x128 / 128x256 (BK 32, two workgroups per CU). By default 5
+ * is taken for <= 128 rows per expert where the 256x256 tile would give few
+ * workgroups, 14 for <= 1024 rows per expert with hidden_dim <= 2048, else 7. */
 int candle_moe_set_tile_policy(int policy);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
- * bits 2-4: the GEMM kernel (policy code above); -1 = invalid sizes. */
+ * bits 2-5: the GEMM kernel (policy code above); -1 = invalid sizes. */
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype);
+
+/* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status
+ * and the FusedMoE forward (hipFreeAsync on the stream each was used on); the
+ * next call allocates again. No counterpart in the reference, whose fused_moe
+ * allocates and frees per call (/root/reference/kernels/moe.cu:570,770). */
+int candle_moe_trim_workspaces(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
 const char* candle_moe_last_error(void);

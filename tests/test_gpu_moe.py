@@ -169,6 +169,26 @@ def test_empty_and_invalid_indices():
     assert_close(got, want, RTOL[O.BF16], "dropped pairs")
 
 
+def test_owned_workspace_reused_grown_and_trimmed():
+    # the library keeps one workspace per (device, stream) between calls:
+    # larger, smaller and larger again on one stream, a second stream, a trim
+    import torch
+
+    H, I, E, k = 128, 64, 8, 2
+    cases = {T: moe_inputs(T, H, I, E, k, O.BF16, 50 + T, O.QWEN3) for T in (48, 3000, 16, 5000)}
+    want = {T: O.fused_moe(*c, E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16, mode=O.MODE_F32ACC)
+            for T, c in cases.items()}
+    side = torch.cuda.Stream()
+    for T in (48, 3000, 16, 5000, 48):
+        assert_close(run_moe(*cases[T], E, k, O.SILU, O.QWEN3, O.BF16), want[T], RTOL[O.BF16], f"default stream T={T}")
+        with torch.cuda.stream(side):
+            got = run_moe(*cases[T], E, k, O.SILU, O.QWEN3, O.BF16)
+        assert_close(got, want[T], RTOL[O.BF16], f"side stream T={T}")
+    candle_moe.trim_workspaces()
+    assert_close(run_moe(*cases[3000], E, k, O.SILU, O.QWEN3, O.BF16), want[3000], RTOL[O.BF16], "after trim")
+    assert_close(run_raw(*cases[16], E, k, O.SILU, O.QWEN3, O.BF16), want[16], RTOL[O.BF16], "raw after trim")
+
+
 def test_deterministic_k2():
     x, G, U, D, rw, ri = moe_inputs(512, 1024, 512, 8, 2, O.BF16, 14, O.QWEN3)
     a = run_moe(x, G, U, D, rw, ri, 8, 2, O.SILU, O.QWEN3, O.BF16)
@@ -267,7 +287,7 @@ def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32, 64, 256, 8, 2, O.F32) == "simt"
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
 @pytest.mark.parametrize("combine", [1, 2])
 def test_tile_configs(tile, combine):
     # both MFMA block tiles on both combine paths, ragged groups and column tails
