@@ -132,7 +132,26 @@ struct Problem {
     int split2;     // K splits of the pair-path down GEMM (atomic combine)
     int n_tiles1, n_tiles2;
     bool lds_family;  // both GEMMs run moe_lds_gemm (fused clears and K splits available)
+    int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
 };
+
+// CUs per XCD of the current device (its CUs over the 8 XCDs of MI355X), 0
+// when unknown; read once per device.
+static int cus_per_xcd() {
+    static std::mutex mu;
+    static int cached[64];
+    static bool known[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!known[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+        cached[dev] = (n > 0 && n % 8 == 0) ? n / 8 : 0;
+        known[dev] = true;
+    }
+    return cached[dev];
+}
 
 struct Layout {
     size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles;
@@ -190,6 +209,10 @@ static Layout make_layout(const Problem& p) {
         const size_t c2 = p.split2 > 1 ? (size_t)mt * p.n_tiles2 : 0;
         L.partial = o; o += a256((t1 > t2 ? t1 : t2) * p.BM * tile_cols(p.cfg) * 4);
         L.counters = o; o += a256((c1 > c2 ? c1 : c2) * 4);
+    } else if (p.tail_cus > 0) {
+        const size_t slots = 8 * (size_t)p.tail_cus;
+        L.partial = o; o += a256(slots * p.BM * tile_cols(p.cfg) * 4);
+        L.counters = o; o += a256(slots * 4);
     }
     L.total = o;
     return L;
@@ -266,6 +289,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
     p.split1 = p.split2 = 1;
+    // tail balance for the 8-wave 256x256 kernel (its K splits meet in the
+    // split-K fixup): the tiles of each XCD's last, partly filled round are
+    // split along K
+    p.tail_cus = (p.lds_family && p.cfg == kLds256w8) ? cus_per_xcd() : 0;
     if (p.lds_family && p.cfg == kLdsRows32 && P > 0) {
         const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);
@@ -300,6 +327,9 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         const long long mt = grouping_max_tiles(p.P, p.E, p.BM);
         gb.zero_ptr = counters;
         gb.zero_n = (int)(mt * (p.n_tiles1 > p.n_tiles2 ? p.n_tiles1 : p.n_tiles2));
+    } else if (p.tail_cus > 0) {
+        gb.zero_ptr = counters;
+        gb.zero_n = 8 * p.tail_cus;
     }
     hipError_t e;
     {
@@ -352,6 +382,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.ksplit = p.split1;
     g1.partial = reinterpret_cast<float*>(ws + L.partial);
     g1.counters = counters;
+    g1.tail_cus = p.tail_cus;
     // the gate/up workgroups clear the pair path's accumulator
     const bool fused_clear = !p.set_path && p.lds_family;
     if (fused_clear) {

@@ -86,7 +86,14 @@ struct GemmArgs {
     float* zero_f32;          // f32 range cleared by this launch's workgroups (null: none)
     long long zero_n;
     int overwrite;            // expert-set down GEMM: out = acc instead of out + acc
+    // Tail balance (8-wave 256x256 kernel): CUs per XCD, 0 = off. The tiles
+    // of each XCD's last, partly filled round are split along K so that the
+    // round's workgroups fill the XCD's CUs; the splits meet in the fixup
+    // through partial [8*tail_cus][BM*BN] f32 and counters [8*tail_cus].
+    int tail_cus;
 };
+constexpr int kTailMaxSplit = 8;
+constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter splits lose to the fixup)
 
 // Kernel shapes. kTileSimt: 64x64 SIMT; kTile128 / kTile256: MFMA kernels
 // with 128x128 / 256x256 block tiles (the grouping tile table must be built

@@ -3,6 +3,8 @@
 // LDS swizzles, XCD-aware tile order and the per-tile epilogues.
 #pragma once
 
+#include <type_traits>
+
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
 
@@ -112,51 +114,113 @@ __device__ __forceinline__ u32x4 tr_pair(const char* p_lo, const char* p_hi) {
     return v;
 }
 
-// Split-K fixup. Every split writes its f32 partial tile to
-// a.partial[tile][ks] (lane-contiguous per register), then counts itself in
-// a.counters[tile]; the split that arrives last sums all partials in split
-// order (so the result does not depend on which split finished last), resets
-// the counter and returns true (it runs the epilogue, once per tile), the
-// others return false. The splits may run on different XCDs, whose L2s are
-// not coherent with each other: the partials are written and read with
-// device-scope relaxed atomics (write-through / L2-bypassing accesses), each
-// thread waits for its stores before the workgroup counts itself, so no
-// L2-wide write-back or invalidate is needed.
-template <int MB, int NB, int NW>
-__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB][NB], int tile, int ks,
+// Split-K fixup. Every split writes its f32 partial tile to partial slot
+// slot0 + ks (per wave, per 32x32 block, 4 registers of a lane as one 16-byte
+// chunk, lanes contiguous), then counts itself in a.counters[ctr]; the split
+// that arrives last sums all partials in split order (so the result does not
+// depend on which split finished last), resets the counter and returns true
+// (it runs the epilogue, once per tile), the others return false. The splits
+// may run on different XCDs, whose L2s are not coherent with each other: the
+// partials are written and read with device-coherent buffer accesses (cache
+// policy sc1: written through to, and read from, the level shared by all
+// XCDs), each thread waits for its stores before the workgroup counts
+// itself, so no L2-wide write-back or invalidate is needed. The accesses are
+// compiler builtins, not inline asm: the stores read MFMA results, whose
+// read-after-write hazards only the compiler knows to pad.
+constexpr int kCachePolicyDevice = 16;  // CPol::SC1
+
+template <int MB, int NB, int NW, int BATCH>
+__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB][NB], int slot0, int ctr, int ks,
                                              int nsplit, int wave, int lane) {
     __shared__ int s_last;
     constexpr int PER_WAVE = MB * NB * 16 * 64;
     constexpr int PER = NW * PER_WAVE;  // floats per workgroup partial (BM * BN)
-    float* mine = a.partial + ((long long)tile * nsplit + ks) * PER + wave * PER_WAVE;
+    constexpr int NQ = MB * NB * 4;     // 16-byte chunks per lane
+    static_assert(NQ % BATCH == 0, "fixup batch");
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(a.partial, 0, 0x7ffffff0, 0x00020000);
+    const uint32_t lane_off = (uint32_t)(wave * PER_WAVE) * 4u + (uint32_t)lane * 16u;
+    const uint32_t mine = (uint32_t)(slot0 + ks) * (uint32_t)PER * 4u + lane_off;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                __hip_atomic_store(mine + ((mb * NB + nb) * 16 + i) * 64 + lane, acc[mb][nb][i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 0; q < NQ; ++q) {
+        const f32x16& r = acc[(q >> 2) / NB][(q >> 2) % NB];
+        const int i = 4 * (q & 3);
+        const u32x4 v = {__float_as_uint(r[i]), __float_as_uint(r[i + 1]), __float_as_uint(r[i + 2]),
+                         __float_as_uint(r[i + 3])};
+        __builtin_amdgcn_raw_buffer_store_b128(v, pr, mine + q * 1024, 0, kCachePolicyDevice);
+    }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+        s_last = __hip_atomic_fetch_add(a.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
     __syncthreads();
     if (!s_last) return false;
-    for (int s2 = 0; s2 < nsplit; ++s2) {
-        float* o = a.partial + ((long long)tile * nsplit + s2) * PER + wave * PER_WAVE;
+    // split 0 replaces the registers, the others add in split order
+    auto gather = [&](int s2, auto first) {
+        const uint32_t src = (uint32_t)(slot0 + s2) * (uint32_t)PER * 4u + lane_off;
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+        for (int q0 = 0; q0 < NQ; q0 += BATCH) {
+            u32x4 v[BATCH];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int b = 0; b < BATCH; ++b)
+                v[b] = __builtin_amdgcn_raw_buffer_load_b128(pr, src + (q0 + b) * 1024, 0, kCachePolicyDevice);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float v = __hip_atomic_load(o + ((mb * NB + nb) * 16 + i) * 64 + lane, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                    acc[mb][nb][i] = s2 == 0 ? v : acc[mb][nb][i] + v;
+            for (int b = 0; b < BATCH; ++b) {
+                const int q = q0 + b;
+                f32x16& r = acc[(q >> 2) / NB][(q >> 2) % NB];
+                const int i = 4 * (q & 3);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float x = __uint_as_float(v[b][j]);
+                    if constexpr (decltype(first)::value) r[i + j] = x;
+                    else r[i + j] += x;
                 }
+            }
+        }
+    };
+    gather(0, std::true_type{});
+    for (int s2 = 1; s2 < nsplit; ++s2) gather(s2, std::false_type{});
+    if (threadIdx.x == 0) __hip_atomic_store(a.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+// Work item of this workgroup under tail balance (GemmArgs::tail_cus = C > 0).
+// XCD x takes a contiguous range of nx of the `live` tiles, as xcd_logical;
+// its first nx - R (R = nx mod C) tiles run whole, in nx / C full rounds over
+// the XCD's C CUs. The R tiles of the last round are split along K into
+// S = min(C / R, 8, K tiles / 8) parts when R <= C / 2, so that R * S workgroups
+// share that round instead of R. Split j of tail tile t of XCD x uses partial
+// slot x*C + t*S + j and counter x*C + t. Returns false for a workgroup
+// without work.
+__device__ __forceinline__ bool tail_item(int live, int C, int nk_all, int& tile, int& ks, int& nsplit, int& slot0,
+                                          int& ctr) {
+    live = min(live, (int)gridDim.x);
+    const int w = blockIdx.x, xcd = w & 7, idx = w >> 3;
+    const int per = live >> 3, rem = live & 7;
+    const int nx = per + (xcd < rem ? 1 : 0);
+    const int base = xcd * per + (xcd < rem ? xcd : rem);
+    const int R = nx % C, full = nx - R;
+    int S = 1;
+    if (R > 0 && 2 * R <= C) S = min(min(C / R, kTailMaxSplit), nk_all / kTailMinKTiles);
+    ks = 0;
+    nsplit = 1;
+    slot0 = ctr = 0;
+    if (S <= 1) {
+        if (idx >= nx) return false;
+        tile = base + idx;
+        return true;
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (idx < full) {
+        tile = base + idx;
+        return true;
+    }
+    const int j = idx - full;
+    if (j >= R * S) return false;
+    const int t = j / S;
+    tile = base + full + t;
+    ks = j - t * S;
+    nsplit = S;
+    ctr = xcd * C + t;
+    slot0 = xcd * C + t * S;
     return true;
 }
 

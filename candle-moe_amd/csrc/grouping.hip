@@ -120,19 +120,22 @@ __device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
 // One workgroup. block_counts[b][e] becomes the number of bin-e items in
 // blocks < b (its base inside the bin's segment): bins go round-robin to the
 // waves, each scans its bin over the blocks 64 at a time. Then the bin totals
-// and tile counts are scanned into offsets and the tile table.
+// and tile counts are scanned into offsets and the tile table. Also clears
+// zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs).
 __global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int nbins, int BM,
                                                                int32_t* __restrict__ block_counts,
                                                                int32_t* __restrict__ offsets,
                                                                int32_t* __restrict__ tile_row,
                                                                int32_t* __restrict__ tile_exp,
-                                                               int32_t* __restrict__ num_tiles) {
+                                                               int32_t* __restrict__ num_tiles,
+                                                               int32_t* __restrict__ zero_ptr, int zero_n) {
     extern __shared__ int32_t s_tot[];  // [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads]
     int32_t* s_tb = s_tot + nbins;
     int32_t* s_part = s_tb + nbins;
     __shared__ int32_t s_max;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (threadIdx.x == 0) s_max = 0;
+    for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
     for (int e = wave; e < nbins; e += kGroupThreads / 64) {
         int32_t carry = 0;
         for (int b0 = 0; b0 < nblocks; b0 += 64) {
@@ -343,10 +346,6 @@ static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int
                            b.zero_n);
         return hipGetLastError();
     }
-    if (b.zero_n > 0) {
-        hipError_t e = launch_fill_zero_bytes(b.zero_ptr, (long long)b.zero_n * 4, stream);
-        if (e != hipSuccess) return e;
-    }
     const int nb = grouping_blocks(items);
     int bbits = 0;
     while ((1 << bbits) < nbins) ++bbits;
@@ -355,7 +354,8 @@ static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int
                            idx, items, k, E, nbins, b.block_counts);
     }
     hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), (2 * nbins + kGroupThreads) * sizeof(int32_t),
-                       stream, nb, nbins, BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles);
+                       stream, nb, nbins, BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles,
+                       b.zero_ptr, b.zero_n);
     if (nb > 0) {
         hipLaunchKernelGGL((grouping_scatter<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t),
                            stream, idx, items, k, E, nbins, bbits, b.block_counts, b.offsets, b.sorted_pair,

@@ -78,10 +78,21 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // workgroup -> (output tile, K split); every workgroup first clears its
     // share of zero_f32 (the accumulator of the GEMM that follows)
     clear_share(a.zero_f32, a.zero_n);
-    const int nsplit = a.ksplit > 1 ? a.ksplit : 1;
-    const int lg = xcd_logical(*a.num_tiles * a.n_tiles * nsplit);
-    if (lg < 0) return;
-    const int tile = lg / nsplit, ks = lg - tile * nsplit;
+    constexpr bool FIXUP = BM <= 32 || NW == 8;  // kernels that carry the split-K fixup
+    int tile, ks, nsplit, fix_slot0, fix_ctr;
+    if (FIXUP && a.tail_cus > 0) {
+        if (!tail_item(*a.num_tiles * a.n_tiles, a.tail_cus, (a.K + BK - 1) / BK, tile, ks, nsplit, fix_slot0,
+                       fix_ctr))
+            return;
+    } else {
+        nsplit = a.ksplit > 1 ? a.ksplit : 1;
+        const int lg = xcd_logical(*a.num_tiles * a.n_tiles * nsplit);
+        if (lg < 0) return;
+        tile = lg / nsplit;
+        ks = lg - tile * nsplit;
+        fix_slot0 = tile * nsplit;
+        fix_ctr = tile;
+    }
     const int mt = tile / a.n_tiles, nt = tile - mt * a.n_tiles;
     const int r0 = a.tile_row[mt];
     const int grp = a.tile_exp[mt];
@@ -370,11 +381,15 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         }
     }
 
-    if constexpr (BM <= 32 || NW == 8) {
+    if constexpr (FIXUP) {
         // split K: the last split to finish a tile sums all partials in split
         // order and alone runs the epilogue (one atomic per output element and
         // pair, as without splits)
-        if (nsplit > 1 && !splitk_fixup<MB, NB, NW>(a, acc, tile, ks, nsplit, wave, lane)) return;
+        // loads in flight per batch: the atomic-combine kernels keep their
+        // row table in registers and have less room
+        constexpr int FIX_BATCH = ATOMIC ? 4 : 8;
+        if (nsplit > 1 && !splitk_fixup<MB, NB, NW, FIX_BATCH>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
+            return;
     }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w);
 }
@@ -382,7 +397,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
 template <int DT, int MODE>
 hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     // one workgroup per (row tile, column tile, K split)
-    const long long nwg_l = (long long)a.m_tiles_max * a.n_tiles * (a.ksplit > 1 ? a.ksplit : 1);
+    // tail balance: each XCD's range plus up to tail_cus split workgroups
+    const long long tiles = (long long)a.m_tiles_max * a.n_tiles;
+    const long long nwg_l = a.tail_cus > 0 ? 8 * ((tiles + 7) / 8 + a.tail_cus)
+                                           : tiles * (a.ksplit > 1 ? a.ksplit : 1);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     const int nwg = (int)nwg_l;
     if (nwg <= 0) return hipSuccess;

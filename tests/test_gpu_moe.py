@@ -189,6 +189,28 @@ def test_owned_workspace_reused_grown_and_trimmed():
     assert_close(run_raw(*cases[16], E, k, O.SILU, O.QWEN3, O.BF16), want[16], RTOL[O.BF16], "raw after trim")
 
 
+@pytest.mark.parametrize("combine", [1, 2])
+def test_tail_balanced_splits(combine):
+    # the 8-wave 256x256 kernel splits the tiles of each XCD's last round
+    # along K (here every gate/up tile: 2 per XCD, 4 splits of 8 K tiles);
+    # the splits meet in the ordered fixup, so the result matches the oracle
+    # and repeats bit for bit
+    T, H, I, E, k = 512, 2048, 256, 8, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 60 + combine, O.QWEN3)
+    kw = dict(E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.BF16)
+    try:
+        candle_moe.set_tile_policy(candle_moe.TILE_W8)
+        candle_moe.set_combine_policy(combine)
+        a = run_moe(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16)
+        b = run_moe(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16)
+    finally:
+        candle_moe.set_tile_policy(0)
+        candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+    assert np.array_equal(a, b)
+    assert_close(a, O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_F32ACC, **kw), RTOL[O.BF16], "f32acc")
+    assert_close(a, O.fused_moe(x, G, U, D, rw, ri, mode=O.MODE_EXACT, **kw), RTOL[O.BF16], "exact")
+
+
 def test_deterministic_k2():
     x, G, U, D, rw, ri = moe_inputs(512, 1024, 512, 8, 2, O.BF16, 14, O.QWEN3)
     a = run_moe(x, G, U, D, rw, ri, 8, 2, O.SILU, O.QWEN3, O.BF16)
