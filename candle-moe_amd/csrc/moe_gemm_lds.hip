@@ -303,9 +303,17 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // K tile's 64 KB reach the L2 at an even rate instead of in one burst
     // that stalls the issuing waves.
     constexpr int PER_STEP = (LOADS + KSTEPS - 1) / KSTEPS;
+    // Otherwise (8 waves): the waves of row group 1 issue the whole DMA of
+    // the next tile after their first k16 step's MFMAs (ds >= 0 only for
+    // them), so that the two waves sharing a SIMD do not both stall on the
+    // memory pipeline right after the barrier (2 % on the prefill GEMMs;
+    // issuing later leaves the DMA too little time before the next barrier).
     auto dma_slice = [&](int ds, int dk, int step) {
         if constexpr (SPREAD) {
             if (ds >= 0) issue_range(ds, dk, step * PER_STEP, (step + 1) * PER_STEP);
+            __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (NW == 8) {
+            if (step == 0 && ds >= 0) issue_range(ds, dk, 0, LOADS);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -376,8 +384,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         if constexpr (SPREAD) {
             compute(kt % NST, ahead < nk ? ahead % NST : -1, (kt0 + ahead) * BK);
         } else {
-            if (ahead < nk) issue(ahead % NST, (kt0 + ahead) * BK);
-            compute(kt % NST, -1, 0);
+            const bool late = NW == 8 && wm == 1;  // row group 1 issues after its first k16 step
+            if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
+            compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
         }
     }
 
