@@ -317,7 +317,19 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    // A wave whose rows all lie past the group's end (the last row tile of a
+    // group) reads no fragments and issues no MFMAs; it still issues its DMA
+    // share and meets every barrier. On a half-empty tile this leaves the
+    // matrix core of each SIMD to the other wave.
+    // (Not in the 4-wave 256x256 kernels, whose 256 accumulators leave no
+    // registers for the second code path.)
+    const bool rows_live = MB * NB > 8 || wm * WM < m_valid;
     auto compute = [&](int stage, int ds, int dk) {
+        if (!rows_live) {
+#pragma unroll
+            for (int st = 0; st < KSTEPS; ++st) dma_slice(ds, dk, st);
+            return;
+        }
         const char* sA = smem + stage * STAGE;
         const char* sB = sA + A_BYTES;
         u32x4 af0[MB], bf0[NB], af1[MB], bf1[NB];
