@@ -290,9 +290,10 @@ def set_combine_policy(policy: int) -> None:
 
 
 (TILE_AUTO, TILE_128, TILE_256, TILE_LDS_256, TILE_LDS_256x128, TILE_LDS_128, TILE_LDS_256K64, TILE_W8, TILE_W8K32,
- TILE_PINGPONG, TILE_W8K32_SPREAD, TILE_K32_SPREAD, TILE_ROWS32, TILE_256x128_OCC2, TILE_128x256_OCC2) = range(15)
+ TILE_PINGPONG, TILE_W8K32_SPREAD, TILE_K32_SPREAD, TILE_ROWS32, TILE_256x128_OCC2, TILE_128x256_OCC2,
+ TILE_F32_ROWS32, TILE_F32_128) = range(17)
 _TILE_ROWS = {0: 64, 1: 128, 2: 256, 3: 256, 4: 256, 5: 128, 6: 256, 7: 256, 8: 256, 9: 256, 10: 256, 11: 256, 12: 32,
-              13: 256, 14: 128}
+              13: 256, 14: 128, 15: 32, 16: 128}
 
 
 def set_tile_policy(policy: int) -> None:

@@ -132,6 +132,7 @@ struct Problem {
     int split2;     // K splits of the pair-path down GEMM (atomic combine)
     int n_tiles1, n_tiles2;
     bool lds_family;  // both GEMMs run moe_lds_gemm (fused clears and K splits available)
+    bool fused_clear_ok;  // the gate/up kernel can clear the pair path's accumulator
     int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
 };
 
@@ -219,7 +220,7 @@ static Layout make_layout(const Problem& p) {
 }
 
 static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
-                         Problem& p) {
+                         Problem& p, bool aligned16 = true) {
     if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
     if (H < 1 || I < 1)
         return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: hidden_dim and intermediate_dim must be >= 1 (got %d, %d)", H, I);
@@ -251,6 +252,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     const long long touched = P < E ? P : E;
     auto est_tiles = [&](int bm) { return std::max<long long>((P + bm - 1) / bm, touched); };
     p.cfg = !p.mfma ? kTileSimt : (g_tile_policy ? g_tile_policy : kLds256w8);
+    // f32: the tiled vector-FMA kernel (32-row tile with K splits for decode,
+    // 128-row tile otherwise) wherever 16-byte loads are possible
+    const bool f32_tiled = p.dtype == kF32 && H % 4 == 0 && I % 4 == 0 && aligned16;
+    if (f32_tiled) {
+        p.cfg = (P <= 32 * touched) ? kF32Rows32 : kF32Tile128;
+        if (g_tile_policy == kF32Rows32 || g_tile_policy == kF32Tile128) p.cfg = g_tile_policy;
+    } else if (!p.mfma || is_f32_cfg(p.cfg)) {
+        p.cfg = kTileSimt;
+    }
     if (p.mfma && !g_tile_policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
@@ -282,10 +292,12 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     }
     // K splits for the 32-row (decode) GEMMs whose expected output tiles
     // (< 128) leave most CUs idle: up to ~256 workgroups, at most 8 splits,
-    // no empty split. Each split writes a 32 KB f32 partial that the last one
-    // sums, so splitting only pays where the weight stream would otherwise run
-    // on a few CUs.
+    // no empty split; for the f32 kernels (< 256 tiles) up to ~512
+    // workgroups and 16 splits. Each split writes an f32 partial tile that
+    // the last one sums, so splitting only pays where the weight stream would
+    // otherwise run on a few CUs.
     p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
+    p.fused_clear_ok = p.lds_family || is_f32_cfg(p.cfg);
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
     p.split1 = p.split2 = 1;
@@ -293,14 +305,18 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // split-K fixup): the tiles of each XCD's last, partly filled round are
     // split along K
     p.tail_cus = (p.lds_family && p.cfg == kLds256w8) ? cus_per_xcd() : 0;
-    if (p.lds_family && p.cfg == kLdsRows32 && P > 0) {
+    if (((p.lds_family && p.cfg == kLdsRows32) || is_f32_cfg(p.cfg)) && P > 0) {
         const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);
+        // the f32 kernel keeps one K chunk in flight per workgroup: twice the
+        // workgroups, up to 16 splits (both tile heights)
+        const bool f32 = is_f32_cfg(p.cfg);
+        const long long target = f32 ? 512 : 256, max_sp = f32 ? 16 : 8;
         auto choose = [&](long long tiles, int K) {
-            if (tiles >= 128) return 1;
+            if (tiles >= target / 2) return 1;
             const int nk = (K + bk - 1) / bk;
-            long long sp = (256 + tiles - 1) / tiles;
-            if (sp > 8) sp = 8;
+            long long sp = (target + tiles - 1) / tiles;
+            if (sp > max_sp) sp = max_sp;
             if (sp > nk) sp = nk;
             if (sp < 1) sp = 1;
             const int per = (int)((nk + sp - 1) / sp);
@@ -384,7 +400,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.counters = counters;
     g1.tail_cus = p.tail_cus;
     // the gate/up workgroups clear the pair path's accumulator
-    const bool fused_clear = !p.set_path && p.lds_family;
+    const bool fused_clear = !p.set_path && p.fused_clear_ok;
     if (fused_clear) {
         g1.zero_f32 = acc;
         g1.zero_n = (long long)p.T * p.H;
@@ -544,7 +560,9 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
                    uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream) {
     clear_error();
     Problem p;
-    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p);
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    const bool aligned16 = a16(x) && a16(gate) && a16(up) && a16(down);
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16);
     if (rc) return rc;
     rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
     if (rc) return rc;
@@ -572,9 +590,11 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
 }
 
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
-    Problem p;
-    if (check_problem(T, H, I, E, k, 0, 0, dtype, p)) return 0;
-    return make_layout(p).total;
+    // the kernel choice may depend on the operands' alignment: enough for either
+    Problem p, q;
+    if (check_problem(T, H, I, E, k, 0, 0, dtype, p, true)) return 0;
+    if (check_problem(T, H, I, E, k, 0, 0, dtype, q, false)) return 0;
+    return std::max(make_layout(p).total, make_layout(q).total);
 }
 
 }  // namespace cm

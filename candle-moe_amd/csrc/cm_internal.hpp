@@ -112,21 +112,25 @@ constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter s
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
     kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11, kLdsRows32 = 12,
-    kLds256x128o2 = 13, kLds128x256o2 = 14
+    kLds256x128o2 = 13, kLds128x256o2 = 14, kF32Rows32 = 15, kF32Tile128 = 16
 };
-constexpr int kNumTileCfgs = 15;
+constexpr int kNumTileCfgs = 17;
+inline bool is_f32_cfg(int cfg) { return cfg == kF32Rows32 || cfg == kF32Tile128; }
 inline int tile_rows(int cfg) {
-    if (cfg == kLdsRows32) return 32;
+    if (cfg == kLdsRows32 || cfg == kF32Rows32) return 32;
+    if (cfg == kF32Tile128) return 128;
     return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds128x256o2) ? 128 : 256);
 }
 inline int tile_cols(int cfg) {
+    if (is_f32_cfg(cfg)) return 128;
     return (cfg == kTileSimt) ? 64
                               : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128 || cfg == kLds256x128o2) ? 128
                                                                                                                     : 256);
 }
-inline bool is_lds_cfg(int cfg) { return cfg >= kLds256; }
+inline bool is_lds_cfg(int cfg) { return cfg >= kLds256 && !is_f32_cfg(cfg); }
 // K tile of the LDS-DMA kernels
 inline int tile_bk(int cfg) {
+    if (is_f32_cfg(cfg)) return 16;
     return (cfg == kLds256 || cfg == kLds256w8k32 || cfg == kLds256w8k32s || cfg == kLds256k32s ||
             cfg == kLds256x128o2 || cfg == kLds128x256o2)
                ? 32
@@ -139,6 +143,7 @@ int gemm_tile_cols(int mode, int cfg);
 hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_pp(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
+hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
 
 // f32 accumulator helpers

@@ -518,6 +518,7 @@ bool mfma_supported(int dtype, int K, int N) {
 
 int gemm_tile_cols(int mode, int cfg) {
     const int bn = tile_cols(cfg);
+    if (is_f32_cfg(cfg)) return mode == kGateUp ? bn / 2 : bn;
     return (mode == kGateUp && cfg != kTileSimt) ? bn / 2 : bn;
 }
 
@@ -559,6 +560,7 @@ static hipError_t launch_dt(int mode, int cfg, const GemmArgs& a, hipStream_t st
 
 hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
     if (is_lds_cfg(cfg)) return launch_moe_gemm_lds(mode, dtype, cfg, a, stream);
+    if (is_f32_cfg(cfg)) return dtype == kF32 ? launch_moe_gemm_f32(mode, cfg, a, stream) : hipErrorInvalidValue;
     if (dtype == kBF16) return launch_dt<kBF16>(mode, cfg, a, stream);
     if (dtype == kF16) return launch_dt<kF16>(mode, cfg, a, stream);
     if (dtype == kF32) return launch_dt<kF32>(mode, cfg, a, stream);

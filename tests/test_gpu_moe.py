@@ -309,6 +309,54 @@ def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32, 64, 256, 8, 2, O.F32) == "simt"
 
 
+@pytest.mark.parametrize("tile", [15, 16])
+def test_f32_tiles(tile):
+    # the f32 vector-FMA kernel at both tile heights: K not a multiple of its
+    # 16-deep chunks, N not a multiple of its 128 (64 for gate/up) columns,
+    # [N,K] fc2 weights (Nomic), top-1
+    try:
+        candle_moe.set_tile_policy(tile)
+        check_case(300, 100, 196, 8, 2, O.F32, O.QWEN3, seed=70 + tile)
+        check_case(200, 132, 76, 6, 2, O.F32, O.NOMIC, act=O.GELU, seed=71 + tile)
+        check_case(40, 64, 48, 8, 1, O.F32, O.QWEN3, seed=72 + tile)
+    finally:
+        candle_moe.set_tile_policy(0)
+
+
+def test_f32_decode_splits_deterministic():
+    # decode: 32-row f32 tiles with K split over several workgroups, ordered fixup
+    T, H, I, E, k = 4, 768, 3072, 8, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.F32, 80, O.NOMIC)
+    a = run_moe(x, G, U, None, rw, ri, E, k, O.GELU, O.NOMIC, O.F32)
+    b = run_moe(x, G, U, None, rw, ri, E, k, O.GELU, O.NOMIC, O.F32)
+    assert np.array_equal(a, b)
+    want = O.fused_moe(x, G, U, None, rw, ri, E=E, k=k, act=O.GELU, moe_type=O.NOMIC, dtype=O.F32,
+                       mode=O.MODE_EXACT)
+    assert_close(a, want, RTOL[O.F32], "f32 decode")
+
+
+def test_f32_unaligned_operands_take_the_scalar_kernel():
+    # 16-byte loads need aligned operands; an input 4 bytes off takes moe_simt_gemm
+    import torch
+
+    T, H, I, E, k = 64, 128, 96, 4, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.F32, 81, O.QWEN3)
+    big = torch.zeros(T * H + 1, dtype=torch.float32, device="cuda:0")
+    big[1:] = to_dev(x).reshape(-1)
+    tg, tu, td, trw, tri = to_dev(G), to_dev(U), to_dev(D), to_dev(rw), to_dev(ri)
+    out = torch.zeros((T, H), dtype=torch.float32, device="cuda:0")
+    L = candle_moe.lib()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    xp = ctypes.c_void_p(big.data_ptr() + 4)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = L.candle_moe_fused_moe_status(xp, p(tg), p(tu), p(td), p(trw), p(tri), p(out), T, H, I, E, k, O.SILU,
+                                       O.QWEN3, O.F32, stream)
+    candle_moe.check(rc)
+    torch.cuda.synchronize()
+    want = O.fused_moe(x, G, U, D, rw, ri, E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=O.F32, mode=O.MODE_EXACT)
+    assert_close(from_dev(out).astype(np.float64), want, RTOL[O.F32], "unaligned f32")
+
+
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
 @pytest.mark.parametrize("combine", [1, 2])
 def test_tile_configs(tile, combine):
