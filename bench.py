@@ -290,12 +290,39 @@ def bench_router_only(args, torch, cm, dev):
         us = 1000.0 * ms[0] / cnt[0]
         nbytes = T * E * 4 + T * k * 12
         res[f"{T}x{E}k{k}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    # router GEMM fused with topk-softmax (hidden [T,H] bf16, Linear weight
+    # [E,H]): bytes = hidden + weight + outputs; HBM-bound on hidden
+    fused = {}
+    for (name, T, H, E, k) in [("qwen3", 32768, 4096, 8, 2), ("nomic", 32768, 768, 8, 2),
+                               ("q30b", 4096, 2048, 128, 8)]:
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed)
+        nbuf = max(1, (512 << 20) // (T * H * 2))
+        xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(nbuf)]
+        wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        w = torch.empty((T, k), device=dev)
+        i = torch.empty((T, k), dtype=torch.int32, device=dev)
+        ei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        for _ in range(args.warmup):
+            cm.router_topk(xs[0], wr, w, i, ei)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        nrep = max(args.steps, 50)
+        ev[0].record()
+        for s in range(nrep):
+            cm.router_topk(xs[s % nbuf], wr, w, i, ei)
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = 1000.0 * ev[0].elapsed_time(ev[1]) / nrep
+        nbytes = T * H * 2 + E * H * 2 + T * k * 12
+        fused[f"{name} T={T} H={H} E={E} k={k}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
     head = res["32768x8k2"]
     print(json.dumps({
         "metric": "topk-softmax µs", "value": head["us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["us"] / 1000.0, "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic N(0,1) logits, cold buffers",
         "config": {"workload": "topk-softmax [32768,E] (config 2)"}, "shapes": res,
+        "router_gemm_topk_bf16": fused,
         "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": None},
         "cpu_baseline": None,

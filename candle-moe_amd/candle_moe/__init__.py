@@ -114,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_profile_end.restype = i32
         L.candle_moe_profile_slot_name.argtypes = [i32]
         L.candle_moe_profile_slot_name.restype = ctypes.c_char_p
+        L.candle_moe_router_topk.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, u32, vp]
+        L.candle_moe_router_topk.restype = i32
         L.candle_moe_trim_workspaces.argtypes = []
         L.candle_moe_trim_workspaces.restype = i32
         L.candle_moe_last_error.argtypes = []
@@ -216,6 +218,31 @@ def apply_topk_softmax_inplace(gating_output, topk_weight, topk_indices, token_e
     g, w, i, ei = (describe(t) for t in (gating_output, topk_weight, topk_indices, token_expert_indices))
     check(lib().candle_moe_apply_topk_softmax_inplace(
         ctypes.byref(g), ctypes.byref(w), ctypes.byref(i), ctypes.byref(ei), _stream_for(gating_output)))
+
+
+def router_topk(hidden, router_weight, topk_weight, topk_indices, token_expert_indices) -> None:
+    """Router GEMM fused with topk-softmax (an extension: the reference's
+    callers compute ``hidden.matmul`` with candle, then call
+    apply_topk_softmax_inplace). hidden [T, H] and router_weight [E, H] (Linear
+    layout) of one dtype, contiguous; logits = dtype(hidden @ router_weight.T)
+    with f32 accumulation; outputs as apply_topk_softmax_inplace with f32
+    topk_weight [T, k]."""
+    for t in (hidden, router_weight, topk_weight, topk_indices, token_expert_indices):
+        if not t.is_contiguous():
+            raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "router_topk: tensors must be contiguous")
+    if router_weight.dtype != hidden.dtype or topk_weight.dtype.itemsize != 4:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "router_topk: router_weight must have hidden's dtype, "
+                             "topk_weight must be f32")
+    T, H = hidden.shape
+    E, k = router_weight.shape[0], topk_weight.shape[1]
+    if router_weight.shape[1] != H or tuple(topk_indices.shape) != (T, k) or \
+            tuple(token_expert_indices.shape) != (T, k) or topk_weight.shape[0] != T:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "router_topk: shape mismatch")
+    check(lib().candle_moe_router_topk(
+        ctypes.c_void_p(hidden.data_ptr()), ctypes.c_void_p(router_weight.data_ptr()),
+        ctypes.c_void_p(topk_weight.data_ptr()), ctypes.c_void_p(topk_indices.data_ptr()),
+        ctypes.c_void_p(token_expert_indices.data_ptr()), T, H, E, k, _torch_dtype_code(hidden),
+        _stream_for(hidden)))
 
 
 def validate_topk_softmax(g: CmTensor, w: CmTensor, i: CmTensor, ei: CmTensor) -> None:

@@ -658,6 +658,33 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
                               activation_type, moe_type, dtype, workspace, workspace_bytes, false, false, stream);
 }
 
+int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight, void* topk_indices,
+                           void* token_expert_indices, int num_tokens, int hidden_dim, int num_experts, int topk,
+                           uint32_t dtype, void* stream) {
+    cm::clear_error();
+    const int T = num_tokens, H = hidden_dim, E = num_experts, k = topk;
+    if (T < 0) return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: num_tokens must be >= 0 (got %d)", T);
+    if (E < 1 || E > 128)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: num_experts must be in [1, 128] (got %d)", E);
+    if (k < 1 || k > E)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: topk must be in [1, num_experts=%d] (got %d)", E, k);
+    if (dtype > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: dtype code must be 0, 1 or 2");
+    const int epv = dtype == cm::kF32 ? 4 : 8;
+    if (H < 1 || H % epv)
+        return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED,
+                             "router_topk: hidden_dim must be a positive multiple of %d for this dtype (got %d)", epv, H);
+    if (T == 0) return CANDLE_MOE_OK;
+    if (!hidden || !router_weight || !topk_weight || !topk_indices || !token_expert_indices)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: null tensor pointer");
+    if (((uintptr_t)hidden | (uintptr_t)router_weight) & 15)
+        return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED, "router_topk: hidden and router_weight must be 16-byte aligned");
+    const hipError_t e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
+                                                reinterpret_cast<uint32_t*>(topk_indices),
+                                                reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k,
+                                                reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "router_topk launch");
+}
+
 int candle_moe_trim_workspaces(void) {
     cm::clear_error();
     return cm::trim_owned_workspaces();

@@ -8,6 +8,8 @@
 namespace cm {
 
 // ---------------------------------------------------------------- router
+hipError_t launch_router_topk(const void* x, const void* w, int dtype, float* wo, uint32_t* io, uint32_t* eo, int T,
+                              int H, int E, int k, hipStream_t stream);
 hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_dtype, uint32_t* idx,
                                uint32_t* ei, int T, int E, int k, hipStream_t stream);
 

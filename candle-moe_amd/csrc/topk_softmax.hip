@@ -22,6 +22,7 @@ namespace cm {
 
 template <int LPR, typename V>
 __device__ __forceinline__ V group_max(V v) {
+    if constexpr (LPR >= 64) v = fmaxf(v, xor_lane<32>(v));
     if constexpr (LPR >= 32) v = fmaxf(v, xor_lane<16>(v));
     if constexpr (LPR >= 16) v = fmaxf(v, xor_lane<8>(v));
     if constexpr (LPR >= 8) v = fmaxf(v, xor_lane<4>(v));
@@ -32,6 +33,7 @@ __device__ __forceinline__ V group_max(V v) {
 
 template <int LPR>
 __device__ __forceinline__ double group_sum(double v) {
+    if constexpr (LPR >= 64) v += xor_lane<32>(v);
     if constexpr (LPR >= 32) v += xor_lane<16>(v);
     if constexpr (LPR >= 16) v += xor_lane<8>(v);
     if constexpr (LPR >= 8) v += xor_lane<4>(v);
@@ -49,6 +51,7 @@ __device__ __forceinline__ void argmax_step(float& v, int& i) {
 
 template <int LPR>
 __device__ __forceinline__ void group_argmax(float& v, int& i) {
+    if constexpr (LPR >= 64) argmax_step<32>(v, i);
     if constexpr (LPR >= 32) argmax_step<16>(v, i);
     if constexpr (LPR >= 16) argmax_step<8>(v, i);
     if constexpr (LPR >= 8) argmax_step<4>(v, i);
@@ -86,25 +89,13 @@ __device__ __forceinline__ void load_row_values(const void* __restrict__ logits,
     }
 }
 
-template <int VPT, int LPR, int INDT, int OUTDT>
-__global__ __launch_bounds__(128) void topk_softmax_kernel(const void* __restrict__ logits,
-                                                          void* __restrict__ wout,
-                                                          uint32_t* __restrict__ iout,
-                                                          uint32_t* __restrict__ eiout, int T, int E,
-                                                          int k, int aligned) {
-    const long long gtid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long row = gtid / LPR;
-    const int g = (int)(gtid % LPR);
-    // Lanes past the last row still take part in the group butterflies
-    // (their group is entirely past the end, so it only reads row T-1).
-    const bool valid = row < T;
-    const long long r = valid ? row : (long long)T - 1;
-    const int e0 = g * VPT;
-    const bool full = aligned && (E == LPR * VPT);
-
-    float x[VPT];
-    load_row_values<VPT, INDT>(logits, r, E, e0, full, x);
-
+// Softmax over one token's E logits held by a group of LPR lanes (lane g of
+// the group: experts e0 .. e0+VPT-1, -inf past E), then the top k in
+// descending order, ties to the lower index; lane j % LPR writes output j.
+template <int VPT, int LPR, int OUTDT>
+__device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
+                                                   long long row, bool valid, void* __restrict__ wout,
+                                                   uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout) {
     float m = x[0];
 #pragma unroll
     for (int j = 1; j < VPT; ++j) m = fmaxf(m, x[j]);
@@ -145,6 +136,28 @@ __global__ __launch_bounds__(128) void topk_softmax_kernel(const void* __restric
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
+__global__ __launch_bounds__(128) void topk_softmax_kernel(const void* __restrict__ logits,
+                                                          void* __restrict__ wout,
+                                                          uint32_t* __restrict__ iout,
+                                                          uint32_t* __restrict__ eiout, int T, int E,
+                                                          int k, int aligned) {
+    const long long gtid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long row = gtid / LPR;
+    const int g = (int)(gtid % LPR);
+    // Lanes past the last row still take part in the group butterflies
+    // (their group is entirely past the end, so it only reads row T-1).
+    const bool valid = row < T;
+    const long long r = valid ? row : (long long)T - 1;
+    const int e0 = g * VPT;
+    const bool full = aligned && (E == LPR * VPT);
+
+    float x[VPT];
+    load_row_values<VPT, INDT>(logits, r, E, e0, full, x);
+
+    softmax_topk_group<VPT, LPR, OUTDT>(x, e0, g, E, k, T, row, valid, wout, iout, eiout);
+}
+
+template <int VPT, int LPR, int INDT, int OUTDT>
 static hipError_t launch_cfg(const void* logits, void* w, uint32_t* idx, uint32_t* ei, int T, int E,
                              int k, hipStream_t stream) {
     constexpr int BLOCK = 128;
@@ -170,6 +183,138 @@ static hipError_t launch_dt(const void* logits, void* w, uint32_t* idx, uint32_t
     if (E <= 256) return launch_cfg<8, 32, INDT, OUTDT>(logits, w, idx, ei, T, E, k, stream);
     if (E <= 512) return launch_cfg<16, 32, INDT, OUTDT>(logits, w, idx, ei, T, E, k, stream);
     return launch_cfg<32, 32, INDT, OUTDT>(logits, w, idx, ei, T, E, k, stream);
+}
+
+// ------------------------------------------------------------------------
+// Router GEMM fused with topk-softmax: logits[t,e] = dtype(sum_h x[t,h] *
+// w[e,h]) with f32 accumulation and one rounding to the input dtype (the
+// output of candle's matmul / Linear in that dtype), then the softmax and
+// top-k above on f32(logits). w is [E,H], candle's Linear weight layout.
+// One wave per TPW tokens: lane l multiplies the 8 (f32: 4) consecutive h at
+// each step's 16-byte chunk l (16-byte loads of x and of the E weight rows,
+// which stay in L2), keeping TPW x EMAX partial sums (f32 FMAs on the
+// converted values); the partials go through
+// LDS ([value][lane], padded) and lane l sums the 64 partials of the logits
+// it owns for the softmax: LPR = 64 / TPW lanes per token, VPT experts each.
+// Bound: HBM reading x (T*H*sizeof(dtype)).
+template <int DT, int EMAX, int TPW>
+__global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict__ xin, const void* __restrict__ win,
+                                                         float* __restrict__ wout, uint32_t* __restrict__ iout,
+                                                         uint32_t* __restrict__ eiout, int T, int H, int E, int k) {
+    typedef typename Elem<DT>::storage S;
+    constexpr int LPR = 64 / TPW;
+    constexpr int VPT = EMAX / LPR;
+    constexpr int NV = TPW * EMAX;  // partial sums per lane
+    constexpr int EPV = 16 / (int)sizeof(S);  // elements per 16-byte load
+    constexpr int EC = 8;                      // weight rows per batch of loads
+    static_assert(VPT * LPR == EMAX && EMAX % EC == 0, "router tile");
+    __shared__ float s_part[NV][65];
+    const int lane = threadIdx.x;
+    const long long t0 = (long long)blockIdx.x * TPW;
+    const S* X = reinterpret_cast<const S*>(xin);
+    const S* W = reinterpret_cast<const S*>(win);
+    // acc += x . w over one 16-byte chunk of each
+    auto dot16 = [](const u32x4& xq, const u32x4& wq, float acc) {
+        if constexpr (DT == kBF16) {
+            // (v_dot2_f32_bf16 / _f16 were tried: they do not return the exact
+            // sum even where every product and partial sum is representable
+            // in f32, so FMAs on converted values)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = fmaf(__uint_as_float(xq[j] << 16), __uint_as_float(wq[j] << 16), acc);
+                acc = fmaf(__uint_as_float(xq[j] & 0xffff0000u), __uint_as_float(wq[j] & 0xffff0000u), acc);
+            }
+        } else if constexpr (DT == kF16) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = fmaf(Elem<kF16>::to_f32((uint16_t)(xq[j] & 0xffffu)), Elem<kF16>::to_f32((uint16_t)(wq[j] & 0xffffu)),
+                           acc);
+                acc = fmaf(Elem<kF16>::to_f32((uint16_t)(xq[j] >> 16)), Elem<kF16>::to_f32((uint16_t)(wq[j] >> 16)), acc);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = fmaf(__uint_as_float(xq[j]), __uint_as_float(wq[j]), acc);
+        }
+        return acc;
+    };
+    float acc[TPW][EMAX];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) acc[t][e] = 0.f;
+    for (int h0 = 0; h0 < H; h0 += 64 * EPV) {
+        const int h = h0 + EPV * lane;
+        const bool hv = h < H;
+        u32x4 xq[TPW];
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            xq[t] = u32x4{0u, 0u, 0u, 0u};
+            if (hv && t0 + t < T) xq[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(X + (t0 + t) * H + h));
+        }
+#pragma unroll
+        for (int e0 = 0; e0 < EMAX; e0 += EC) {
+            if (e0 >= E) break;
+            u32x4 wq[EC];
+#pragma unroll
+            for (int j = 0; j < EC; ++j) {
+                wq[j] = u32x4{0u, 0u, 0u, 0u};
+                if (hv && e0 + j < E) wq[j] = *reinterpret_cast<const u32x4*>(W + (long long)(e0 + j) * H + h);
+            }
+#pragma unroll
+            for (int j = 0; j < EC; ++j)
+#pragma unroll
+                for (int t = 0; t < TPW; ++t) acc[t][e0 + j] = dot16(xq[t], wq[j], acc[t][e0 + j]);
+        }
+    }
+    // transpose-reduce through LDS: value v = t*EMAX + e of every lane
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) s_part[t * EMAX + e][lane] = acc[t][e];
+    __syncthreads();
+    const int tl = lane / LPR, g = lane % LPR, e0 = g * VPT;
+    float x[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int e = e0 + j;
+        float sum = 0.f;
+        for (int i = 0; i < 64; ++i) sum += s_part[tl * EMAX + e][i];
+        // the logit as the matmul would store it in the input dtype
+        x[j] = e < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+    }
+    const long long row = t0 + tl;
+    const bool valid = row < T;
+    softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
+}
+
+template <int DT, int EMAX, int TPW>
+static hipError_t launch_router_cfg(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
+                                    int H, int E, int k, hipStream_t stream) {
+    const long long grid = (T + TPW - 1) / TPW;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((router_topk_kernel<DT, EMAX, TPW>), dim3((unsigned)grid), dim3(64), 0, stream, x, w, wo, io,
+                       eo, T, H, E, k);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_router_dt(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
+                                   int H, int E, int k, hipStream_t stream) {
+    if (E <= 8) return launch_router_cfg<DT, 8, 8>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (E <= 16) return launch_router_cfg<DT, 16, 4>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (E <= 32) return launch_router_cfg<DT, 32, 2>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (E <= 64) return launch_router_cfg<DT, 64, 1>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (E <= 128) return launch_router_cfg<DT, 128, 1>(x, w, wo, io, eo, T, H, E, k, stream);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_router_topk(const void* x, const void* w, int dtype, float* wo, uint32_t* io, uint32_t* eo, int T,
+                              int H, int E, int k, hipStream_t stream) {
+    if (T == 0) return hipSuccess;
+    if (dtype == kBF16) return launch_router_dt<kBF16>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (dtype == kF16) return launch_router_dt<kF16>(x, w, wo, io, eo, T, H, E, k, stream);
+    if (dtype == kF32) return launch_router_dt<kF32>(x, w, wo, io, eo, T, H, E, k, stream);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_dtype, uint32_t* idx,

@@ -147,6 +147,20 @@ int candle_moe_set_tile_policy(int policy);
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype);
 
+/* Router GEMM fused with topk-softmax (no counterpart symbol in the
+ * reference; its callers compute the logits with a separate candle matmul,
+ * /root/reference/README.md:61-71, then call topk_softmax on them):
+ *   logits[t,e] = dtype(sum_h hidden[t,h] * router_weight[e,h])   (f32 accumulation,
+ *                 one rounding to dtype, as candle's Linear in that dtype stores them)
+ *   then topk_softmax of f32(logits): topk_weight f32 [T,k], topk_indices u32 [T,k],
+ *   token_expert_indices u32 [T,k] = j*T + t.
+ *   hidden [T,H], router_weight [E,H] (candle Linear layout), both `dtype`,
+ *   16-byte aligned; H a multiple of 8 (4 for f32); 1 <= E <= 128.
+ * Reads hidden once (HBM-bound); the logits never reach memory. */
+int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight,
+                           void* topk_indices, void* token_expert_indices, int num_tokens,
+                           int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);
+
 /* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status
  * and the FusedMoE forward (hipFreeAsync on the stream each was used on); the
  * next call allocates again. No counterpart in the reference, whose fused_moe

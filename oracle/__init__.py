@@ -118,6 +118,20 @@ def topk_softmax(logits: np.ndarray, k: int, literal: bool = False):
     return w, i, ei
 
 
+def router_logits(x: np.ndarray, w: np.ndarray, dtype: int) -> np.ndarray:
+    """Router logits as candle's Linear in `dtype` produces them for the
+    callers of topk_softmax (/root/reference/README.md:61-71 usage: logits
+    from a separate matmul, then apply_topk_softmax_inplace): x [T,H] and
+    w [E,H] (Linear layout) as dtype storage; the products summed exactly (f64
+    here; f32 accumulation on the GPU agrees wherever the f32 sum is exact),
+    rounded once to dtype, returned as f32 [T,E]. Pinned in
+    tests/test_oracle.py by one-hot rows (logit = the weight column, which a
+    transposed operand fails) and scaling."""
+    xf = to_f32(x, dtype).astype(np.float64)
+    wf = to_f32(w, dtype).astype(np.float64)
+    return round_to((xf @ wf.T).astype(np.float32), dtype)
+
+
 def preprocess(idx: np.ndarray, w: np.ndarray, E: int):
     """Grouping oracle: (offsets[E+2], sorted_tok, sorted_w, sorted_pair)."""
     idx = np.ascontiguousarray(idx, dtype=np.uint32)

@@ -1,0 +1,115 @@
+"""Router GEMM fused with topk-softmax (candle_moe_router_topk) on the GPU.
+
+The fused op computes logits = dtype(hidden @ router_weight.T) with f32
+accumulation and feeds them to the same softmax / top-k as topk_softmax.
+
+* Exact cases: inputs k/8 and j/64 (small integers over powers of two), so
+  every product and every partial sum is exact in f32 and the GPU's
+  accumulation order cannot matter: indices and token_expert_indices must be
+  bit-exact and weights within 1e-6 relative of the oracle (router_logits,
+  then topk_softmax). The discrete values also produce tied logits, which
+  exercise the lower-index tie rule.
+* Random normal cases: logits within the f32 accumulation error of a dtype
+  rounding point may round either way; tokens with such a logit (or with a
+  top-k margin inside that error, for f32) are set aside, must be few, and
+  every other token must match as above.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import candle_moe
+import oracle as O
+from helpers import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def run_fused(x, w, k, dt):
+    import torch
+
+    T, E = x.shape[0], w.shape[0]
+    xt, wt = to_dev(x, dt), to_dev(w, dt)
+    tw = torch.full((T, k), -7.0, dtype=torch.float32, device="cuda:0")
+    ti = torch.full((T, k), -1, dtype=torch.int32, device="cuda:0")
+    te = torch.full((T, k), -1, dtype=torch.int32, device="cuda:0")
+    candle_moe.router_topk(xt, wt, tw, ti, te)
+    torch.cuda.synchronize()
+    return from_dev(tw), from_dev(ti).astype(np.uint32), from_dev(te).astype(np.uint32)
+
+
+def quantized(shape, denom, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.integers(-8, 9, shape) / denom).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
+@pytest.mark.parametrize("T,H,E,k", [(1000, 4096, 8, 2), (333, 768, 8, 2), (129, 2048, 128, 8), (77, 1024, 64, 6),
+                                     (50, 512, 16, 4), (40, 256, 32, 3), (9, 64, 5, 5)])
+def test_router_topk_exact(dt, T, H, E, k):
+    x = O.to_dtype(quantized((T, H), 8.0, T + H), dt)
+    w = O.to_dtype(quantized((E, H), 64.0, E + k), dt)
+    gw, gi, ge = run_fused(x, w, k, dt)
+    ww, wi, we = O.topk_softmax(O.router_logits(x, w, dt), k)
+    assert np.array_equal(gi, wi)
+    assert np.array_equal(ge, we)
+    np.testing.assert_allclose(gw, ww, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F32])
+def test_router_topk_random_normal(dt):
+    T, H, E, k = 4096, 2048, 8, 2
+    rng = np.random.default_rng(9)
+    xf = rng.standard_normal((T, H)).astype(np.float32)
+    wf = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
+    x, w = O.to_dtype(xf, dt), O.to_dtype(wf, dt)
+    gw, gi, ge = run_fused(x, w, k, dt)
+    # The GPU's f32 sums may differ from the exact ones by accumulation
+    # roundoff; a logit whose exact value lies within that distance of a dtype
+    # rounding point may round either way. err: 16 roundoff units of the sum
+    # of magnitudes (the worst case of the GPU's 32 + 64 term summation is 96;
+    # the kernel is deterministic, so a bound that holds once holds always).
+    x64, w64 = O.to_f32(x, dt).astype(np.float64), O.to_f32(w, dt).astype(np.float64)
+    exact = x64 @ w64.T
+    err = 16 * 2.0 ** -24 * (np.abs(x64) @ np.abs(w64).T)
+    near = O.round_to(exact.astype(np.float32), dt)
+    lo = O.round_to((exact - err).astype(np.float32), dt)
+    hi = O.round_to((exact + err).astype(np.float32), dt)
+    n_amb = (lo != hi).sum(axis=1)
+    if dt == O.F32:
+        # f32 logits are not rounded: instead a near-tie inside the error can
+        # reorder the top k
+        srt = np.sort(exact, axis=1)[:, ::-1]
+        n_amb = n_amb * 0 + 2 * ((srt[:, :k] - srt[:, 1:k + 1]).min(axis=1) < 2 * err.max(axis=1))
+    cands = [O.topk_softmax(c, k) for c in (near, lo, hi)]
+    checked = 0
+    for t in range(T):
+        if n_amb[t] >= 2:
+            continue
+        ok = [np.array_equal(gi[t], c[1][t]) and np.allclose(gw[t], c[0][t], rtol=2e-5 if dt == O.F32 else 1e-6, atol=0)
+              for c in (cands if n_amb[t] else cands[:1])]
+        assert any(ok), (t, gi[t], cands[0][1][t], gw[t], cands[0][0][t])
+        checked += 1
+    assert checked > 0.8 * T, checked
+    assert np.array_equal(ge, cands[0][2])
+
+
+def test_router_topk_errors():
+    import torch
+
+    L = candle_moe.lib()
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device="cuda:0")
+    w = torch.zeros((200, 64), dtype=torch.bfloat16, device="cuda:0")
+    out = torch.zeros((4, 2), dtype=torch.float32, device="cuda:0")
+    idx = torch.zeros((4, 2), dtype=torch.int32, device="cuda:0")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 4, 64, 200, 2, O.BF16, s) != 0
+    assert "num_experts" in candle_moe.last_error()
+    assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 4, 60, 8, 2, O.BF16, s) != 0
+    assert "multiple of 8" in candle_moe.last_error()
+    xo = ctypes.c_void_p(x.data_ptr() + 2)
+    assert L.candle_moe_router_topk(xo, p(w), p(out), p(idx), p(idx), 2, 64, 8, 2, O.BF16, s) != 0
+    assert "aligned" in candle_moe.last_error()
+    assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 0, 64, 8, 2, O.BF16, s) == 0

@@ -266,3 +266,33 @@ def test_golden_fixtures_reproduce():
                              E=int(z["E"]), k=int(z["k"]), act=int(z["act"]), moe_type=int(z["moe_type"]),
                              dtype=dt, mode=O.MODE_EXACT)
             assert np.allclose(ex, z["out_exact"], rtol=1e-12, atol=1e-12), f
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
+def test_router_logits_one_hot_and_scaling(dt):
+    # a one-hot row h picks column h of every expert's weight row: logits[t, e]
+    # = w[e, h_t] (already dtype values), which the transposed product fails;
+    # twice the row gives twice the logits (exact in every dtype)
+    T, H, E = 24, 40, 6
+    rng = np.random.default_rng(5)
+    w = O.to_dtype(rng.standard_normal((E, H)).astype(np.float32), dt)
+    h = rng.integers(0, H, T)
+    x1 = np.zeros((T, H), np.float32)
+    x1[np.arange(T), h] = 1.0
+    got = O.router_logits(O.to_dtype(x1, dt), w, dt)
+    wf = O.to_f32(w, dt)
+    assert np.array_equal(got, wf[:, h].T)
+    got2 = O.router_logits(O.to_dtype(2 * x1, dt), w, dt)
+    assert np.array_equal(got2, 2 * wf[:, h].T)
+
+
+def test_router_logits_round_once_to_dtype():
+    # sums of exactly representable products: the exact sum, rounded once
+    x = np.array([[1.0, 1.0 / 512.0, 1.0 / 512.0]], np.float32)
+    w = np.array([[1.0, 1.0, 1.0]], np.float32)
+    # 1 + 2^-8 is a bf16 tie (ulp 2^-7 at 1): round to even -> 1.0
+    got = O.router_logits(O.to_dtype(x, O.BF16), O.to_dtype(w, O.BF16), O.BF16)
+    assert got[0, 0] == 1.0
+    # f32 keeps it
+    got = O.router_logits(x, w, O.F32)
+    assert got[0, 0] == np.float32(1.0 + 2.0 ** -8)
