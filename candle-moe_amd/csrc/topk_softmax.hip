@@ -90,9 +90,9 @@ __device__ __forceinline__ void load_row_values(const void* __restrict__ logits,
 }
 
 // Softmax over one token's E logits held by a group of LPR lanes (lane g of
-// the group: experts e0 .. e0+VPT-1, -inf past E), then the top k in
+// the group: experts e0 + q*ESTR, q < VPT, -inf past E), then the top k in
 // descending order, ties to the lower index; lane j % LPR writes output j.
-template <int VPT, int LPR, int OUTDT>
+template <int VPT, int LPR, int OUTDT, int ESTR = 1>
 __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
                                                    long long row, bool valid, void* __restrict__ wout,
                                                    uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout) {
@@ -106,13 +106,13 @@ __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const float d = x[j] - m;
-        p[j] = (e0 + j < E) ? (float)exp((double)d) : 0.0f;
+        p[j] = (e0 + j * ESTR < E) ? (float)exp((double)d) : 0.0f;
         s += (double)p[j];
     }
     s = group_sum<LPR>(s);
     const float S = (float)s;
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) p[j] = (e0 + j < E) ? p[j] / S : -1.0f;
+    for (int j = 0; j < VPT; ++j) p[j] = (e0 + j * ESTR < E) ? p[j] / S : -1.0f;
 
     typedef typename Elem<OUTDT>::storage WS;
     WS* wo = reinterpret_cast<WS*>(wout);
@@ -121,7 +121,7 @@ __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0
         int bi = e0;
 #pragma unroll
         for (int q = 1; q < VPT; ++q)
-            if (p[q] > bv) { bv = p[q]; bi = e0 + q; }
+            if (p[q] > bv) { bv = p[q]; bi = e0 + q * ESTR; }
         group_argmax<LPR>(bv, bi);
         if (valid && g == (j % LPR)) {
             const long long o = row * (long long)k + j;
@@ -131,7 +131,7 @@ __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0
         }
 #pragma unroll
         for (int q = 0; q < VPT; ++q)
-            if (e0 + q == bi) p[q] = -2.0f;
+            if (e0 + q * ESTR == bi) p[q] = -2.0f;
     }
 }
 
@@ -197,6 +197,30 @@ static hipError_t launch_dt(const void* logits, void* w, uint32_t* idx, uint32_t
 // LDS ([value][lane], padded) and lane l sums the 64 partials of the logits
 // it owns for the softmax: LPR = 64 / TPW lanes per token, VPT experts each.
 // Bound: HBM reading x (T*H*sizeof(dtype)).
+// Reduce-scatter of 64 values over the 64 lanes of a wave: afterwards lane l
+// holds the wave-wide sum of value l. At the step for lane bit b the lanes
+// with that bit set keep the upper half of the remaining values, the others
+// the lower half, and each adds its partner's copy of the half it keeps.
+template <int HALF>
+__device__ __forceinline__ void reduce_scatter_step(float* v, int lane) {
+    const bool hi = (lane & HALF) != 0;
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+        const float a = v[i], b = v[i + HALF];
+        const float send = hi ? a : b;
+        v[i] = (hi ? b : a) + xor_lane<HALF>(send);
+    }
+}
+__device__ __forceinline__ float reduce_scatter64(float (&v)[64], int lane) {
+    reduce_scatter_step<32>(v, lane);
+    reduce_scatter_step<16>(v, lane);
+    reduce_scatter_step<8>(v, lane);
+    reduce_scatter_step<4>(v, lane);
+    reduce_scatter_step<2>(v, lane);
+    reduce_scatter_step<1>(v, lane);
+    return v[0];
+}
+
 template <int DT, int EMAX, int TPW>
 __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict__ xin, const void* __restrict__ win,
                                                          float* __restrict__ wout, uint32_t* __restrict__ iout,
@@ -208,11 +232,12 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
     constexpr int EPV = 16 / (int)sizeof(S);  // elements per 16-byte load
     constexpr int EC = 8;                      // weight rows per batch of loads
     static_assert(VPT * LPR == EMAX && EMAX % EC == 0, "router tile");
-    __shared__ float s_part[NV][65];
+    constexpr bool RS = (NV == 64);  // reduce-scatter in registers, else through LDS
+    __shared__ float s_part[RS ? 1 : NV][65];
     const int lane = threadIdx.x;
-    const long long t0 = (long long)blockIdx.x * TPW;
     const S* X = reinterpret_cast<const S*>(xin);
     const S* W = reinterpret_cast<const S*>(win);
+    const long long t0 = (long long)blockIdx.x * TPW;
     // acc += x . w over one 16-byte chunk of each
     auto dot16 = [](const u32x4& xq, const u32x4& wq, float acc) {
         if constexpr (DT == kBF16) {
@@ -253,7 +278,7 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
         }
 #pragma unroll
         for (int e0 = 0; e0 < EMAX; e0 += EC) {
-            if (e0 >= E) break;
+            if (e0 >= E) continue;
             u32x4 wq[EC];
 #pragma unroll
             for (int j = 0; j < EC; ++j) {
@@ -266,33 +291,125 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
                 for (int t = 0; t < TPW; ++t) acc[t][e0 + j] = dot16(xq[t], wq[j], acc[t][e0 + j]);
         }
     }
-    // transpose-reduce through LDS: value v = t*EMAX + e of every lane
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) s_part[t * EMAX + e][lane] = acc[t][e];
-    __syncthreads();
     const int tl = lane / LPR, g = lane % LPR, e0 = g * VPT;
     float x[VPT];
+    if constexpr (RS) {
+        // lane l = t*EMAX + e receives logit (t, e): LPR = EMAX, VPT = 1
+        const float sum = reduce_scatter64(reinterpret_cast<float(&)[64]>(acc), lane);
+        x[0] = e0 < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+    } else {
+        // transpose-reduce through LDS: value v = t*EMAX + e of every lane
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int e = e0 + j;
-        float sum = 0.f;
-        for (int i = 0; i < 64; ++i) sum += s_part[tl * EMAX + e][i];
-        // the logit as the matmul would store it in the input dtype
-        x[j] = e < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+        for (int t = 0; t < TPW; ++t)
+#pragma unroll
+            for (int e = 0; e < EMAX; ++e) s_part[t * EMAX + e][lane] = acc[t][e];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int e = e0 + j;
+            float sum = 0.f;
+            for (int i = 0; i < 64; ++i) sum += s_part[tl * EMAX + e][i];
+            // the logit as the matmul would store it in the input dtype
+            x[j] = e < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+        }
     }
     const long long row = t0 + tl;
     const bool valid = row < T;
     softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
 }
 
+// 16-bit router on the matrix cores: one wave per 32 tokens, the E experts
+// padded to NB blocks of 32 columns, v_mfma_f32_32x32x16 with both operands
+// straight from global memory: the K order inside each 32-wide chunk is
+// permuted identically for x and the weight rows (lane half hh takes the 16
+// consecutive h at 16*hh, as two MFMA k16 steps), so that every lane loads 32
+// contiguous bytes of its row. The result layout puts expert 32c + l%32 of
+// token 8(i/4) + 4(l/32) + i%4 in register i of block c of lane l, so each
+// register is one token per 32-lane half: the softmax runs 16 times over
+// 32-lane groups (VPT = NB experts per lane, stride 32).
+template <int DT, int NB>
+__global__ __launch_bounds__(256) void router_mfma_kernel(const void* __restrict__ xin,
+                                                          const void* __restrict__ win,
+                                                          float* __restrict__ wout, uint32_t* __restrict__ iout,
+                                                          uint32_t* __restrict__ eiout, int T, int H, int E, int k) {
+    typedef typename Elem<DT>::storage S;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long long t0 = ((long long)blockIdx.x * 4 + wave) * 32;
+    if (t0 >= T) return;  // whole wave
+    const int r = lane & 31, hh = lane >> 5;
+    const long long xrow = t0 + r < T ? t0 + r : (long long)T - 1;  // rows past T compute garbage, unused
+    const S* xr = reinterpret_cast<const S*>(xin) + xrow * H + 16 * hh;
+    const S* wr[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+        wr[c] = reinterpret_cast<const S*>(win) + (long long)(r + 32 * c < E ? r + 32 * c : 0) * H + 16 * hh;
+    f32x16 acc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[c][i] = 0.f;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    // D chunks of 32 h in flight: the loads of chunk c + D are issued as
+    // chunk c is consumed (slot = chunk % D, unrolled so slots are registers)
+    constexpr int D = NB == 1 ? 8 : (NB == 2 ? 4 : 2);
+    u32x4 xa[D][2], wb[D][NB][2];
+    auto load = [&](int sl, int ch) {
+        const int k0 = ch * 32;
+        const bool in0 = k0 + 16 * hh < H, in1 = k0 + 16 * hh + 8 < H;
+        xa[sl][0] = in0 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0)) : z;
+        xa[sl][1] = in1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0 + 8)) : z;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            const bool ev = r + 32 * c < E;
+            wb[sl][c][0] = (ev && in0) ? *reinterpret_cast<const u32x4*>(wr[c] + k0) : z;
+            wb[sl][c][1] = (ev && in1) ? *reinterpret_cast<const u32x4*>(wr[c] + k0 + 8) : z;
+        }
+    };
+    const int nch = (H + 31) / 32;
+#pragma unroll
+    for (int sl = 0; sl < D; ++sl)
+        if (sl < nch) load(sl, sl);
+    for (int c0 = 0; c0 < nch; c0 += D) {
+#pragma unroll
+        for (int sl = 0; sl < D; ++sl) {
+            if (c0 + sl < nch) {
+#pragma unroll
+                for (int c = 0; c < NB; ++c) {
+                    acc[c] = mfma32<DT>(xa[sl][0], wb[sl][c][0], acc[c]);
+                    acc[c] = mfma32<DT>(xa[sl][1], wb[sl][c][1], acc[c]);
+                }
+                if (c0 + sl + D < nch) load(sl, c0 + sl + D);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const long long row = t0 + 8 * (i / 4) + 4 * hh + (i % 4);
+        const bool valid = row < T;
+        float x[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+            x[c] = r + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(acc[c][i])) : -__builtin_inff();
+        softmax_topk_group<NB, 32, kF32, 32>(x, r, r, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
+    }
+}
+
+template <int DT, int NB>
+static hipError_t launch_router_mfma(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
+                                     int H, int E, int k, hipStream_t stream) {
+    const long long grid = ((long long)T + 127) / 128;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((router_mfma_kernel<DT, NB>), dim3((unsigned)grid), dim3(256), 0, stream, x, w, wo, io, eo, T,
+                       H, E, k);
+    return hipGetLastError();
+}
+
 template <int DT, int EMAX, int TPW>
 static hipError_t launch_router_cfg(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                     int H, int E, int k, hipStream_t stream) {
-    const long long grid = (T + TPW - 1) / TPW;
-    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((router_topk_kernel<DT, EMAX, TPW>), dim3((unsigned)grid), dim3(64), 0, stream, x, w, wo, io,
+    const long long groups = (T + TPW - 1) / TPW;
+    if (groups > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((router_topk_kernel<DT, EMAX, TPW>), dim3((unsigned)groups), dim3(64), 0, stream, x, w, wo, io,
                        eo, T, H, E, k);
     return hipGetLastError();
 }
@@ -300,6 +417,13 @@ static hipError_t launch_router_cfg(const void* x, const void* w, float* wo, uin
 template <int DT>
 static hipError_t launch_router_dt(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                    int H, int E, int k, hipStream_t stream) {
+    // 16-bit with more than 32 experts: the matrix-core kernel (2.5x faster
+    // than the FMA kernel at E=128); up to 32 experts the FMA kernel, whose
+    // coalesced row loads beat the MFMA kernel's strided fragments 2x
+    if constexpr (DT != kF32) {
+        if (E > 32 && E <= 64) return launch_router_mfma<DT, 2>(x, w, wo, io, eo, T, H, E, k, stream);
+        if (E > 64) return launch_router_mfma<DT, 4>(x, w, wo, io, eo, T, H, E, k, stream);
+    }
     if (E <= 8) return launch_router_cfg<DT, 8, 8>(x, w, wo, io, eo, T, H, E, k, stream);
     if (E <= 16) return launch_router_cfg<DT, 16, 4>(x, w, wo, io, eo, T, H, E, k, stream);
     if (E <= 32) return launch_router_cfg<DT, 32, 2>(x, w, wo, io, eo, T, H, E, k, stream);
