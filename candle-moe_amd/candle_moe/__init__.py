@@ -110,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_path.restype = i32
         L.candle_moe_profile_begin.argtypes = []
         L.candle_moe_profile_begin.restype = i32
+        L.candle_moe_profile_begin_slots.argtypes = [u32]
+        L.candle_moe_profile_begin_slots.restype = i32
         L.candle_moe_profile_end.argtypes = [vp, vp, i32]
         L.candle_moe_profile_end.restype = i32
         L.candle_moe_profile_slot_name.argtypes = [i32]

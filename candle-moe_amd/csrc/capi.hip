@@ -57,6 +57,7 @@ struct ProfRec {
 };
 static std::mutex g_prof_mu;
 static bool g_prof_on = false;
+static uint32_t g_prof_mask = ~0u;  // slots bracketed while profiling is on
 static std::vector<ProfRec> g_prof;
 static std::vector<hipEvent_t> g_event_pool;  // events of finished sessions, reused (creation costs host time)
 
@@ -75,7 +76,7 @@ struct ProfScope {
     bool on;
     ProfScope(int slot, hipStream_t stream) : s(stream), on(false) {
         std::lock_guard<std::mutex> lk(g_prof_mu);
-        if (!g_prof_on) return;
+        if (!g_prof_on || !((g_prof_mask >> slot) & 1u)) return;
         rec.slot = slot;
         if (!pooled_event_locked(rec.a)) return;
         if (!pooled_event_locked(rec.b)) {
@@ -716,6 +717,14 @@ int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_d
 int candle_moe_profile_begin(void) {
     std::lock_guard<std::mutex> lk(cm::g_prof_mu);
     cm::g_prof_on = true;
+    cm::g_prof_mask = ~0u;
+    return cm::kNumSlots;
+}
+
+int candle_moe_profile_begin_slots(uint32_t slot_mask) {
+    std::lock_guard<std::mutex> lk(cm::g_prof_mu);
+    cm::g_prof_on = true;
+    cm::g_prof_mask = slot_mask;
     return cm::kNumSlots;
 }
 

@@ -118,6 +118,9 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
  * those events and returns, per slot, the summed milliseconds and the number
  * of launches; begin() returns the number of slots. */
 int candle_moe_profile_begin(void);
+/* As profile_begin, bracketing only the slots whose bit is set in slot_mask
+ * (fewer event records in a timed region). */
+int candle_moe_profile_begin_slots(uint32_t slot_mask);
 int candle_moe_profile_end(double* total_ms, int* counts, int nslots);
 const char* candle_moe_profile_slot_name(int slot);
 
