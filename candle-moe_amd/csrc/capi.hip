@@ -349,11 +349,6 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         gb.zero_n = 8 * p.tail_cus;
     }
     hipError_t e;
-    {
-        ProfScope ps(kSlotGroup, s);
-        e = launch_grouping(idx, p.P, p.E, p.BM, gb, s);
-    }
-    if (e != hipSuccess) return hip_fail(e, "fused_moe grouping");
 
     const bool qwen3 = p.moe_type == kQwen3;
     const int m_tiles_max = (int)grouping_max_tiles(p.P, p.E, p.BM);
@@ -369,12 +364,16 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         tb.tile_exp = reinterpret_cast<int32_t*>(ws + L.tile_key2);
         tb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles2);
         pair_dest = reinterpret_cast<int32_t*>(ws + L.pair_dest);
-        {
-            ProfScope ps(kSlotGroup, s);
-            e = launch_token_grouping(idx, p.T, p.k, p.E, p.nkeys, p.BM, tb, pair_dest, s);
-        }
-        if (e != hipSuccess) return hip_fail(e, "fused_moe expert-set grouping");
     }
+    {
+        // pairs by expert and, on the expert-set path, tokens by expert set
+        const GroupJob pj = pair_grouping_job(idx, p.P, p.E, p.BM, gb);
+        GroupJob tj = {};
+        if (p.set_path) tj = set_grouping_job(idx, p.T, p.k, p.E, p.nkeys, p.BM, tb, pair_dest);
+        ProfScope ps(kSlotGroup, s);
+        e = launch_groupings(pj, p.set_path ? &tj : nullptr, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "fused_moe grouping");
 
     GemmArgs g1 = {};
     g1.A = x;

@@ -28,22 +28,34 @@ struct GroupingBufs {
     int zero_n;
 };
 constexpr int kGroupChunk = 1024;      // items per workgroup of the multi-workgroup grouping
-constexpr int kGroupSmallMax = 4096;   // up to this many items: one-workgroup grouping
+constexpr int kGroupSmallMax = 2048;   // up to this many items: one-workgroup grouping
 inline int grouping_blocks(long long P) { return (int)((P + kGroupChunk - 1) / kGroupChunk); }
 // Row tiles of a grouping: sum over non-empty groups of ceil(count / BM)
 // <= ceil(P / BM) + (number of non-empty groups).
 inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM - 1) / BM + (P < E ? P : E); }
-hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
-                           hipStream_t stream);
-
 // Tokens grouped by their expert set: the key of token t is its k expert
 // ids sorted ascending (ids >= E become E and sort last), read as base-(E+1)
 // digits. b.sorted_pair receives the token of each sorted position,
 // pair_dest[t*k + j] = pos(t)*k + rank of slot j in the token's sorted set.
 constexpr int kSetMaxK = 8;
 constexpr int kSetMaxKeys = 1024;
-hipError_t launch_token_grouping(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
-                                 int32_t* pair_dest, hipStream_t stream);
+
+// A grouping job: pairs by expert (k = 1, nbins = E) or tokens by expert set
+// (nbins = (E+1)^k keys, pair_dest set); small = one workgroup does it all,
+// else nb workgroups of kGroupChunk items.
+struct GroupJob {
+    const uint32_t* idx;
+    long long items;
+    int k, E, nbins, ebits, BM, nb;
+    int small;
+    GroupingBufs b;
+    int32_t* pair_dest;
+};
+GroupJob pair_grouping_job(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b);
+GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
+                          int32_t* pair_dest);
+// The pair grouping and optionally the token grouping, in at most three launches.
+hipError_t launch_groupings(const GroupJob& pairs, const GroupJob* tokens, hipStream_t stream);
 
 // ----------------------------------------------------------- grouped GEMM
 enum GemmMode : int {

@@ -9,18 +9,21 @@
 // deterministic), and the multi-block path scans per-block counts instead of
 // aliasing counts and offsets (/root/reference/kernels/preprocessing.cuh:296-298).
 //
-// Up to kGroupSmallMax items one workgroup does everything (grouping_small).
-// Beyond that, three launches, no host synchronisation:
-//   1. grouping_hist   : each workgroup histograms kGroupChunk items in LDS
-//   2. grouping_scan   : one workgroup turns the per-block counts into
-//                        per-block bases (one wave-wide scan per bin), the bin
-//                        offsets and the tile table
-//   3. grouping_scatter: each workgroup re-reads its chunk and ranks items
-//                        stably: 64-lane peer masks from ballots inside a wave,
-//                        per-wave running counts in LDS, one barrier to turn
-//                        the per-wave counts into bases
-// The same three kernels group tokens by their expert set (TOK = true) for
-// the expert-set down projection.
+// Up to kGroupSmallMax items one workgroup does everything (small_body).
+// Beyond that, three phases, no host synchronisation:
+//   1. hist_body   : each workgroup histograms kGroupChunk items in LDS
+//   2. scan_body   : one workgroup turns the per-block counts into per-block
+//                    bases (one wave-wide scan per bin), the bin offsets and
+//                    the tile table
+//   3. scatter_body: each workgroup re-reads its chunk and ranks items
+//                    stably: 64-lane peer masks from ballots inside a wave,
+//                    per-wave running counts in LDS, one barrier to turn the
+//                    per-wave counts into bases
+// The same code groups tokens by their expert set (TOK = true) for the
+// expert-set down projection. The pair grouping and the token grouping share
+// three launches (grouping_hist_k, grouping_mid_k, grouping_scatter_k), each
+// workgroup serving one of the two jobs; a small job runs whole in the
+// middle launch, so decode groupings take one launch.
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
 
@@ -66,15 +69,17 @@ __device__ __forceinline__ int item_bin(const uint32_t* __restrict__ idx, long l
     }
 }
 
+// Histogram of block blk of job j into s_cnt ([4 waves][nbins] of LDS).
 template <bool TOK>
-__global__ __launch_bounds__(kGroupThreads) void grouping_hist(const uint32_t* __restrict__ idx, long long P,
-                                                               int k, int E, int nbins,
-                                                               int32_t* __restrict__ block_counts) {
-    extern __shared__ int32_t s_cnt[];  // [4 waves][nbins]
+__device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
+    const uint32_t* __restrict__ idx = j.idx;
+    const long long P = j.items;
+    const int k = j.k, E = j.E, nbins = j.nbins;
+    int32_t* __restrict__ block_counts = j.b.block_counts;
     const int wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
     __syncthreads();
-    const long long base = (long long)blockIdx.x * kGroupChunk;
+    const long long base = (long long)blk * kGroupChunk;
     const long long end = base + kGroupChunk < P ? base + kGroupChunk : P;
     int32_t* mine = s_cnt + wave * nbins;
     int rank[kSetMaxK];
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_hist(const uint32_t* _
     }
     __syncthreads();
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads)
-        block_counts[(long long)blockIdx.x * nbins + e] =
+        block_counts[(long long)blk * nbins + e] =
             s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
 }
 
@@ -122,14 +127,16 @@ __device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
 // waves, each scans its bin over the blocks 64 at a time. Then the bin totals
 // and tile counts are scanned into offsets and the tile table. Also clears
 // zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs).
-__global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int nbins, int BM,
-                                                               int32_t* __restrict__ block_counts,
-                                                               int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ tile_row,
-                                                               int32_t* __restrict__ tile_exp,
-                                                               int32_t* __restrict__ num_tiles,
-                                                               int32_t* __restrict__ zero_ptr, int zero_n) {
-    extern __shared__ int32_t s_tot[];  // [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads]
+__device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
+    // LDS: [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads]
+    const int nblocks = j.nb, nbins = j.nbins, BM = j.BM;
+    int32_t* __restrict__ block_counts = j.b.block_counts;
+    int32_t* __restrict__ offsets = j.b.offsets;
+    int32_t* __restrict__ tile_row = j.b.tile_row;
+    int32_t* __restrict__ tile_exp = j.b.tile_exp;
+    int32_t* __restrict__ num_tiles = j.b.num_tiles;
+    int32_t* __restrict__ zero_ptr = j.b.zero_ptr;
+    const int zero_n = j.b.zero_n;
     int32_t* s_tb = s_tot + nbins;
     int32_t* s_part = s_tb + nbins;
     __shared__ int32_t s_max;
@@ -183,21 +190,23 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scan(int nblocks, int 
 // the per-wave counts become per-wave bases (block base of the bin + counts
 // of the waves before), and every item goes to base + its rank.
 template <bool TOK>
-__global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t* __restrict__ idx, long long P,
-                                                                  int k, int E, int nbins, int ebits,
-                                                                  const int32_t* __restrict__ block_counts,
-                                                                  const int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ sorted_pair,
-                                                                  int32_t* __restrict__ pair_dest) {
+__device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
     constexpr int NW = kGroupThreads / 64;
     constexpr int IPT = kGroupChunk / kGroupThreads;  // items per lane
-    extern __shared__ int32_t s_wc[];                  // [NW][nbins] per-wave counts, then bases
+    // LDS s_wc: [NW][nbins] per-wave counts, then bases
+    const uint32_t* __restrict__ idx = j.idx;
+    const long long P = j.items;
+    const int k = j.k, E = j.E, nbins = j.nbins, ebits = j.ebits;
+    const int32_t* __restrict__ block_counts = j.b.block_counts;
+    const int32_t* __restrict__ offsets = j.b.offsets;
+    int32_t* __restrict__ sorted_pair = j.b.sorted_pair;
+    int32_t* __restrict__ pair_dest = j.pair_dest;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_wc[i] = 0;
     __syncthreads();
     int32_t* mine = s_wc + wave * nbins;
-    const long long wbase = (long long)blockIdx.x * kGroupChunk + wave * 64 * IPT;
+    const long long wbase = (long long)blk * kGroupChunk + wave * 64 * IPT;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int bin[IPT], lrank[IPT];
     int rank[kSetMaxK];
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t
     }
     __syncthreads();
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
-        int32_t run = offsets[e] + block_counts[(long long)blockIdx.x * nbins + e];
+        int32_t run = offsets[e] + block_counts[(long long)blk * nbins + e];
         for (int w = 0; w < NW; ++w) {
             const int32_t c = s_wc[w * nbins + e];
             s_wc[w * nbins + e] = run;
@@ -249,16 +258,17 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_scatter(const uint32_t
 // the tile table, and the stable ballot scatter. Also clears zero_n ints at
 // zero_ptr (the split-K arrival counters of the GEMMs that follow).
 template <bool TOK>
-__global__ __launch_bounds__(kGroupThreads) void grouping_small(const uint32_t* __restrict__ idx, int P, int k,
-                                                                int E, int nbins, int ebits, int BM,
-                                                                int32_t* __restrict__ offsets,
-                                                                int32_t* __restrict__ sorted_pair,
-                                                                int32_t* __restrict__ tile_row,
-                                                                int32_t* __restrict__ tile_exp,
-                                                                int32_t* __restrict__ num_tiles,
-                                                                int32_t* __restrict__ pair_dest,
-                                                                int32_t* __restrict__ zero_ptr, int zero_n) {
-    extern __shared__ int32_t s_mem[];
+__device__ void small_body(const GroupJob& j, int32_t* s_mem) {
+    const uint32_t* __restrict__ idx = j.idx;
+    const int P = (int)j.items, k = j.k, E = j.E, nbins = j.nbins, ebits = j.ebits, BM = j.BM;
+    int32_t* __restrict__ offsets = j.b.offsets;
+    int32_t* __restrict__ sorted_pair = j.b.sorted_pair;
+    int32_t* __restrict__ tile_row = j.b.tile_row;
+    int32_t* __restrict__ tile_exp = j.b.tile_exp;
+    int32_t* __restrict__ num_tiles = j.b.num_tiles;
+    int32_t* __restrict__ pair_dest = j.pair_dest;
+    int32_t* __restrict__ zero_ptr = j.b.zero_ptr;
+    const int zero_n = j.b.zero_n;
     int32_t* s_cnt = s_mem;               // [4][nbins] per-wave histogram, then per-wave step counts
     int32_t* s_off = s_mem + 4 * nbins;   // [nbins] bin offsets -> running positions
     int32_t* s_tb = s_off + nbins;        // [nbins] tile bases
@@ -333,46 +343,81 @@ __global__ __launch_bounds__(kGroupThreads) void grouping_small(const uint32_t* 
     }
 }
 
-template <bool TOK>
-static hipError_t grouping_impl(const uint32_t* idx, long long items, int k, int E, int nbins, int BM,
-                                const GroupingBufs& b, int32_t* pair_dest, hipStream_t stream) {
-    int bbits0 = 0;
-    while ((1 << bbits0) < nbins) ++bbits0;
-    // LDS of the one-workgroup path: 6 * nbins + threads ints
-    if (items <= kGroupSmallMax && (6LL * nbins + kGroupThreads) * 4 <= 64 * 1024) {
-        hipLaunchKernelGGL((grouping_small<TOK>), dim3(1), dim3(kGroupThreads),
-                           (6 * nbins + kGroupThreads) * sizeof(int32_t), stream, idx, (int)items, k, E, nbins, bbits0,
-                           BM, b.offsets, b.sorted_pair, b.tile_row, b.tile_exp, b.num_tiles, pair_dest, b.zero_ptr,
-                           b.zero_n);
-        return hipGetLastError();
+// The three launches serve the pair grouping (A) and, on the expert-set path,
+// the token grouping (B) together: workgroups [0, A.nb) work on A and the rest
+// on B; in the middle launch workgroup 0 is A's scan (or its whole grouping if
+// A is small) and workgroup 1 the same for B.
+__global__ __launch_bounds__(kGroupThreads) void grouping_hist_k(GroupJob A, GroupJob B) {
+    extern __shared__ int32_t s_dyn[];
+    const int a_nb = A.small ? 0 : A.nb;
+    if ((int)blockIdx.x < a_nb) hist_body<false>(A, blockIdx.x, s_dyn);
+    else hist_body<true>(B, blockIdx.x - a_nb, s_dyn);
+}
+__global__ __launch_bounds__(kGroupThreads) void grouping_mid_k(GroupJob A, GroupJob B, int has_b) {
+    extern __shared__ int32_t s_dyn[];
+    if (blockIdx.x == 0) {
+        if (A.small) small_body<false>(A, s_dyn);
+        else scan_body(A, s_dyn);
+    } else if (has_b) {
+        if (B.small) small_body<true>(B, s_dyn);
+        else scan_body(B, s_dyn);
     }
-    const int nb = grouping_blocks(items);
-    int bbits = 0;
-    while ((1 << bbits) < nbins) ++bbits;
-    if (nb > 0) {
-        hipLaunchKernelGGL((grouping_hist<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t), stream,
-                           idx, items, k, E, nbins, b.block_counts);
+}
+__global__ __launch_bounds__(kGroupThreads) void grouping_scatter_k(GroupJob A, GroupJob B) {
+    extern __shared__ int32_t s_dyn[];
+    const int a_nb = A.small ? 0 : A.nb;
+    if ((int)blockIdx.x < a_nb) scatter_body<false>(A, blockIdx.x, s_dyn);
+    else scatter_body<true>(B, blockIdx.x - a_nb, s_dyn);
+}
+
+static GroupJob make_job(const uint32_t* idx, long long items, int k, int E, int nbins, int BM,
+                         const GroupingBufs& b, int32_t* pair_dest) {
+    GroupJob j = {};
+    j.idx = idx;
+    j.items = items;
+    j.k = k;
+    j.E = E;
+    j.nbins = nbins;
+    j.BM = BM;
+    j.b = b;
+    j.pair_dest = pair_dest;
+    while ((1 << j.ebits) < nbins) ++j.ebits;
+    // one workgroup does everything up to kGroupSmallMax items (LDS of the
+    // one-workgroup path: 6 * nbins + threads ints)
+    j.small = items <= kGroupSmallMax && (6LL * nbins + kGroupThreads) * 4 <= 64 * 1024;
+    j.nb = grouping_blocks(items);
+    return j;
+}
+
+GroupJob pair_grouping_job(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b) {
+    return make_job(idx, P, 1, E, E, BM, b, nullptr);
+}
+
+GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
+                          int32_t* pair_dest) {
+    return make_job(idx, T, k, E, nkeys, BM, b, pair_dest);
+}
+
+hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t stream) {
+    if (B && (B->k < 1 || B->k > kSetMaxK || B->nbins > kSetMaxKeys)) return hipErrorInvalidValue;
+    GroupJob b = B ? *B : GroupJob{};
+    if (!B) b.small = true;  // nothing of B in the multi-workgroup launches
+    const int nb_multi = (A.small ? 0 : A.nb) + (b.small ? 0 : b.nb);
+    auto ints = [](long long n) { return (size_t)n * sizeof(int32_t); };
+    const int bins_multi = std::max(A.small ? 0 : A.nbins, b.small ? 0 : b.nbins);
+    if (nb_multi > 0) {
+        hipLaunchKernelGGL(grouping_hist_k, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins_multi), stream, A, b);
     }
-    hipLaunchKernelGGL(grouping_scan, dim3(1), dim3(kGroupThreads), (2 * nbins + kGroupThreads) * sizeof(int32_t),
-                       stream, nb, nbins, BM, b.block_counts, b.offsets, b.tile_row, b.tile_exp, b.num_tiles,
-                       b.zero_ptr, b.zero_n);
-    if (nb > 0) {
-        hipLaunchKernelGGL((grouping_scatter<TOK>), dim3(nb), dim3(kGroupThreads), 4 * nbins * sizeof(int32_t),
-                           stream, idx, items, k, E, nbins, bbits, b.block_counts, b.offsets, b.sorted_pair,
-                           pair_dest);
+    auto mid_lds = [&](const GroupJob& j) {
+        return j.small ? 6LL * j.nbins + kGroupThreads : 2LL * j.nbins + kGroupThreads;
+    };
+    const long long mid = std::max(mid_lds(A), B ? mid_lds(*B) : 0LL);
+    hipLaunchKernelGGL(grouping_mid_k, dim3(B ? 2 : 1), dim3(kGroupThreads), ints(mid), stream, A, b, B ? 1 : 0);
+    if (nb_multi > 0) {
+        hipLaunchKernelGGL(grouping_scatter_k, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins_multi), stream, A,
+                           b);
     }
     return hipGetLastError();
-}
-
-hipError_t launch_grouping(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b,
-                           hipStream_t stream) {
-    return grouping_impl<false>(idx, P, 1, E, E, BM, b, nullptr, stream);
-}
-
-hipError_t launch_token_grouping(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
-                                 int32_t* pair_dest, hipStream_t stream) {
-    if (k < 1 || k > kSetMaxK || nkeys > kSetMaxKeys) return hipErrorInvalidValue;
-    return grouping_impl<true>(idx, T, k, E, nkeys, BM, b, pair_dest, stream);
 }
 
 }  // namespace cm
