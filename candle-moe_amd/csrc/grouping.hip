@@ -30,6 +30,7 @@
 namespace cm {
 
 constexpr int kGroupThreads = 256;
+constexpr int kScanStageMax = 8192;  // block counts staged in LDS by the scan (32 KB)
 
 // Token t's expert set: its k ids with ids >= E replaced by E, sorted
 // ascending (stable in j); the key reads them as base-(E+1) digits, most
@@ -128,7 +129,10 @@ __device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
 // and tile counts are scanned into offsets and the tile table. Also clears
 // zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs).
 __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
-    // LDS: [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads]
+    // LDS: [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads],
+    // then (when it fits) the [nblocks][nbins] block counts, staged so that each
+    // bin is scanned by one thread from LDS; otherwise bins go round-robin to
+    // the waves, which scan them from global memory 64 blocks at a time
     const int nblocks = j.nb, nbins = j.nbins, BM = j.BM;
     int32_t* __restrict__ block_counts = j.b.block_counts;
     int32_t* __restrict__ offsets = j.b.offsets;
@@ -141,21 +145,43 @@ __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
     int32_t* s_part = s_tb + nbins;
     __shared__ int32_t s_max;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ncounts = nblocks * nbins;
+    const bool staged = ncounts <= kScanStageMax;
+    int32_t* s_bc = s_part + kGroupThreads;
     if (threadIdx.x == 0) s_max = 0;
     for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
-    for (int e = wave; e < nbins; e += kGroupThreads / 64) {
+    if (staged) {
+        for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) s_bc[i] = block_counts[i];
+        __syncthreads();
+    }
+    if (staged) {
+        // one thread per bin walks its column of the staged counts (the LDS
+        // reads are independent, only the running sum is serial)
+        for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+            int32_t run = 0;
+            for (int b = 0; b < nblocks; ++b) {
+                const int32_t c = s_bc[b * nbins + e];
+                s_bc[b * nbins + e] = run;
+                run += c;
+            }
+            s_tot[e] = run;
+            s_tb[e] = (run + BM - 1) / BM;
+        }
+    }
+    int32_t* bc = block_counts;
+    for (int e = wave; e < (staged ? 0 : nbins); e += kGroupThreads / 64) {
         int32_t carry = 0;
         for (int b0 = 0; b0 < nblocks; b0 += 64) {
             const int b = b0 + lane;
             const long long o = (long long)b * nbins + e;
-            const int32_t c = b < nblocks ? block_counts[o] : 0;
+            const int32_t c = b < nblocks ? bc[o] : 0;
             int32_t incl = c;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
                 const int32_t t = __shfl_up(incl, d);
                 if (lane >= d) incl += t;
             }
-            if (b < nblocks) block_counts[o] = carry + incl - c;
+            if (b < nblocks) bc[o] = carry + incl - c;
             carry += __shfl(incl, 63);
         }
         if (lane == 0) {
@@ -164,6 +190,8 @@ __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
         }
     }
     __syncthreads();
+    if (staged)
+        for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) block_counts[i] = s_bc[i];
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) atomicMax(&s_max, s_tot[e]);
     const int32_t total = block_exclusive_scan(s_tot, nbins, s_part);
     const int32_t tiles = block_exclusive_scan(s_tb, nbins, s_part);
@@ -210,10 +238,15 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int bin[IPT], lrank[IPT];
     int rank[kSetMaxK];
+    // the bins first, so that the loads of all IPT items are in flight together
 #pragma unroll
     for (int s = 0; s < IPT; ++s) {
         const long long p = wbase + s * 64 + lane;
-        const int b = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+    }
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        const int b = bin[s];
         const bool active = b >= 0;
         const uint32_t e = active ? (uint32_t)b : 0xffffffffu;
         uint64_t peers = __ballot(active);
@@ -227,7 +260,6 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
         // stores the new one (LDS instructions of a wave execute in order)
         const int before = active ? mine[b] : 0;
         if (active && r == 0) mine[b] = before + __popcll(peers);
-        bin[s] = b;
         lrank[s] = before + r;
     }
     __syncthreads();
@@ -409,7 +441,9 @@ hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t st
         hipLaunchKernelGGL(grouping_hist_k, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins_multi), stream, A, b);
     }
     auto mid_lds = [&](const GroupJob& j) {
-        return j.small ? 6LL * j.nbins + kGroupThreads : 2LL * j.nbins + kGroupThreads;
+        const long long counts = (long long)j.nb * j.nbins;
+        return j.small ? 6LL * j.nbins + kGroupThreads
+                       : 2LL * j.nbins + kGroupThreads + (counts <= kScanStageMax ? counts : 0);
     };
     const long long mid = std::max(mid_lds(A), B ? mid_lds(*B) : 0LL);
     hipLaunchKernelGGL(grouping_mid_k, dim3(B ? 2 : 1), dim3(kGroupThreads), ints(mid), stream, A, b, B ? 1 : 0);
