@@ -312,10 +312,11 @@ def bench_router_only(args, torch, cm, dev):
     # [E,H]): bytes = hidden + weight + outputs; HBM-bound on hidden
     fused = {}
     for (name, T, H, E, k) in [("qwen3", 32768, 4096, 8, 2), ("nomic", 32768, 768, 8, 2),
-                               ("q30b", 4096, 2048, 128, 8)]:
+                               ("q30b", 32768, 2048, 128, 8), ("q30b", 4096, 2048, 128, 8),
+                               ("q30b", 128, 2048, 128, 8), ("q30b", 16, 2048, 128, 8)]:
         g = torch.Generator(device=dev)
         g.manual_seed(args.seed)
-        nbuf = max(1, (512 << 20) // (T * H * 2))
+        nbuf = min(64, max(1, (512 << 20) // (T * H * 2)))
         xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(nbuf)]
         wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         w = torch.empty((T, k), device=dev)

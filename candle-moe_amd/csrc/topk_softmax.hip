@@ -318,24 +318,31 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
     softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
 }
 
-// 16-bit router on the matrix cores: one wave per 32 tokens, the E experts
+// 16-bit router on the matrix cores: one workgroup per 32 tokens, KW waves
+// splitting K (wave w takes the 32-wide chunks w, w+KW, ...), the E experts
 // padded to NB blocks of 32 columns, v_mfma_f32_32x32x16 with both operands
 // straight from global memory: the K order inside each 32-wide chunk is
 // permuted identically for x and the weight rows (lane half hh takes the 16
 // consecutive h at 16*hh, as two MFMA k16 steps), so that every lane loads 32
 // contiguous bytes of its row. The result layout puts expert 32c + l%32 of
-// token 8(i/4) + 4(l/32) + i%4 in register i of block c of lane l, so each
-// register is one token per 32-lane half: the softmax runs 16 times over
-// 32-lane groups (VPT = NB experts per lane, stride 32).
-template <int DT, int NB>
-__global__ __launch_bounds__(256) void router_mfma_kernel(const void* __restrict__ xin,
-                                                          const void* __restrict__ win,
-                                                          float* __restrict__ wout, uint32_t* __restrict__ iout,
-                                                          uint32_t* __restrict__ eiout, int T, int H, int E, int k) {
+// token 8(i/4) + 4(l/32) + i%4 in register i of block c of lane l. The KW
+// partial sums meet in LDS (summed in wave order: deterministic); wave w then
+// takes registers i of [16w/KW, 16(w+1)/KW), each one token per 32-lane half,
+// for the softmax over 32-lane groups (VPT = NB experts per lane, stride 32).
+// Every workgroup reads the whole weight (E*H*2 bytes) once from L2, so the
+// K split (rather than fewer tokens per workgroup) is what spreads a small
+// batch over more waves.
+template <int DT, int NB, int KW, int D>
+__global__ __launch_bounds__(64 * KW) void router_mfma_kernel(const void* __restrict__ xin,
+                                                              const void* __restrict__ win,
+                                                              float* __restrict__ wout, uint32_t* __restrict__ iout,
+                                                              uint32_t* __restrict__ eiout, int T, int H, int E,
+                                                              int k) {
+    static_assert(KW == 4 || KW == 8, "waves");
     typedef typename Elem<DT>::storage S;
+    __shared__ float red[KW][NB][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const long long t0 = ((long long)blockIdx.x * 4 + wave) * 32;
-    if (t0 >= T) return;  // whole wave
+    const long long t0 = (long long)blockIdx.x * 32;  // < T (grid = ceil(T/32))
     const int r = lane & 31, hh = lane >> 5;
     const long long xrow = t0 + r < T ? t0 + r : (long long)T - 1;  // rows past T compute garbage, unused
     const S* xr = reinterpret_cast<const S*>(xin) + xrow * H + 16 * hh;
@@ -349,12 +356,12 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const void* __restrict
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[c][i] = 0.f;
     const u32x4 z = {0u, 0u, 0u, 0u};
-    // D chunks of 32 h in flight: the loads of chunk c + D are issued as
-    // chunk c is consumed (slot = chunk % D, unrolled so slots are registers)
-    constexpr int D = NB == 1 ? 8 : (NB == 2 ? 4 : 2);
+    // D of this wave's chunks in flight: the loads of its chunk j + D are
+    // issued as chunk j is consumed (slot = j % D, unrolled so slots are
+    // registers)
     u32x4 xa[D][2], wb[D][NB][2];
-    auto load = [&](int sl, int ch) {
-        const int k0 = ch * 32;
+    auto load = [&](int sl, int j) {
+        const int k0 = (wave + KW * j) * 32;
         const bool in0 = k0 + 16 * hh < H, in1 = k0 + 16 * hh + 8 < H;
         xa[sl][0] = in0 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0)) : z;
         xa[sl][1] = in1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0 + 8)) : z;
@@ -366,30 +373,43 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const void* __restrict
         }
     };
     const int nch = (H + 31) / 32;
+    const int mine = nch > wave ? (nch - wave + KW - 1) / KW : 0;  // this wave's chunks
 #pragma unroll
     for (int sl = 0; sl < D; ++sl)
-        if (sl < nch) load(sl, sl);
-    for (int c0 = 0; c0 < nch; c0 += D) {
+        if (sl < mine) load(sl, sl);
+    for (int j0 = 0; j0 < mine; j0 += D) {
 #pragma unroll
         for (int sl = 0; sl < D; ++sl) {
-            if (c0 + sl < nch) {
+            if (j0 + sl < mine) {
 #pragma unroll
                 for (int c = 0; c < NB; ++c) {
                     acc[c] = mfma32<DT>(xa[sl][0], wb[sl][c][0], acc[c]);
                     acc[c] = mfma32<DT>(xa[sl][1], wb[sl][c][1], acc[c]);
                 }
-                if (c0 + sl + D < nch) load(sl, c0 + sl + D);
+                if (j0 + sl + D < mine) load(sl, j0 + sl + D);
             }
         }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int c = 0; c < NB; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[wave][c][i][lane] = acc[c][i];
+    __syncthreads();
+    constexpr int RPW = 16 / KW;  // result registers per wave
+#pragma unroll
+    for (int ii = 0; ii < RPW; ++ii) {
+        const int i = RPW * wave + ii;
         const long long row = t0 + 8 * (i / 4) + 4 * hh + (i % 4);
         const bool valid = row < T;
         float x[NB];
 #pragma unroll
-        for (int c = 0; c < NB; ++c)
-            x[c] = r + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(acc[c][i])) : -__builtin_inff();
+        for (int c = 0; c < NB; ++c) {
+            float sum = red[0][c][i][lane];
+#pragma unroll
+            for (int w = 1; w < KW; ++w) sum += red[w][c][i][lane];
+            // the logit as the matmul would store it in the input dtype
+            x[c] = r + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+        }
         softmax_topk_group<NB, 32, kF32, 32>(x, r, r, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
     }
 }
@@ -397,10 +417,16 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const void* __restrict
 template <int DT, int NB>
 static hipError_t launch_router_mfma(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                      int H, int E, int k, hipStream_t stream) {
-    const long long grid = ((long long)T + 127) / 128;
+    const long long grid = ((long long)T + 31) / 32;
     if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((router_mfma_kernel<DT, NB>), dim3((unsigned)grid), dim3(256), 0, stream, x, w, wo, io, eo, T,
-                       H, E, k);
+    // fewer workgroups than CUs: 8 waves per workgroup, otherwise 4
+    constexpr int D = NB == 2 ? 4 : 3;
+    if (grid < 256)
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 8, D>), dim3((unsigned)grid), dim3(512), 0, stream, x, w, wo,
+                           io, eo, T, H, E, k);
+    else
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 4, D>), dim3((unsigned)grid), dim3(256), 0, stream, x, w, wo,
+                           io, eo, T, H, E, k);
     return hipGetLastError();
 }
 
