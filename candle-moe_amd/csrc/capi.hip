@@ -673,6 +673,10 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
     if (H < 1 || H % epv)
         return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED,
                              "router_topk: hidden_dim must be a positive multiple of %d for this dtype (got %d)", epv, H);
+    // the matrix-core kernel addresses 32 rows of hidden and the whole weight
+    // with 31-bit byte offsets
+    if (H > (1 << 22))
+        return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED, "router_topk: hidden_dim must be <= 4194304 (got %d)", H);
     if (T == 0) return CANDLE_MOE_OK;
     if (!hidden || !router_weight || !topk_weight || !topk_indices || !token_expert_indices)
         return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: null tensor pointer");

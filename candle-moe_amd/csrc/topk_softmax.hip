@@ -17,46 +17,90 @@
 // ds_swizzle), so no LDS and no barriers are used.
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
+#include "cm_lds.hpp"
 
 namespace cm {
 
-template <int LPR, typename V>
-__device__ __forceinline__ V group_max(V v) {
-    if constexpr (LPR >= 64) v = fmaxf(v, xor_lane<32>(v));
-    if constexpr (LPR >= 32) v = fmaxf(v, xor_lane<16>(v));
-    if constexpr (LPR >= 16) v = fmaxf(v, xor_lane<8>(v));
-    if constexpr (LPR >= 8) v = fmaxf(v, xor_lane<4>(v));
-    if constexpr (LPR >= 4) v = fmaxf(v, xor_lane<2>(v));
-    if constexpr (LPR >= 2) v = fmaxf(v, xor_lane<1>(v));
+// Lane-group exchange step M (1, 2, 4, 8, 16, 32): a and b are the values of
+// a lane pair that straddles the two halves of an aligned group of 2M lanes
+// (quad xor 1 / 2 by DPP quad_perm, mirror inside 8 / 16 lanes by DPP
+// row_half_mirror / row_mirror, the row swaps of v_permlane16 / 32_swap);
+// both lanes of a pair get the same (a, b). All VALU, no LDS round trip.
+// A symmetric combine of (a, b) over the steps M < LPR leaves every lane of
+// an LPR-lane group with the reduction of the whole group.
+template <int M>
+__device__ __forceinline__ void lane_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+    if constexpr (M == 16 || M == 32) {
+        const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
+                               : __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        constexpr int ctrl = M == 1 ? 0xB1 : (M == 2 ? 0x4E : (M == 4 ? 0x141 : 0x140));
+        a = v;
+        b = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, false);
+    }
+}
+
+template <int M>
+__device__ __forceinline__ float max_step(float v) {
+    uint32_t a, b;
+    lane_pair<M>(__float_as_uint(v), a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+template <int M>
+__device__ __forceinline__ double sum_step(double v) {
+    const uint64_t u = __double_as_longlong(v);
+    uint32_t al, bl, ah, bh;
+    lane_pair<M>((uint32_t)u, al, bl);
+    lane_pair<M>((uint32_t)(u >> 32), ah, bh);
+    // a + b in the same order on both lanes of the pair: identical sums
+    return __longlong_as_double(((uint64_t)ah << 32) | al) + __longlong_as_double(((uint64_t)bh << 32) | bl);
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (LPR >= 2) v = max_step<1>(v);
+    if constexpr (LPR >= 4) v = max_step<2>(v);
+    if constexpr (LPR >= 8) v = max_step<4>(v);
+    if constexpr (LPR >= 16) v = max_step<8>(v);
+    if constexpr (LPR >= 32) v = max_step<16>(v);
+    if constexpr (LPR >= 64) v = max_step<32>(v);
     return v;
 }
 
 template <int LPR>
 __device__ __forceinline__ double group_sum(double v) {
-    if constexpr (LPR >= 64) v += xor_lane<32>(v);
-    if constexpr (LPR >= 32) v += xor_lane<16>(v);
-    if constexpr (LPR >= 16) v += xor_lane<8>(v);
-    if constexpr (LPR >= 8) v += xor_lane<4>(v);
-    if constexpr (LPR >= 4) v += xor_lane<2>(v);
-    if constexpr (LPR >= 2) v += xor_lane<1>(v);
+    if constexpr (LPR >= 2) v = sum_step<1>(v);
+    if constexpr (LPR >= 4) v = sum_step<2>(v);
+    if constexpr (LPR >= 8) v = sum_step<4>(v);
+    if constexpr (LPR >= 16) v = sum_step<8>(v);
+    if constexpr (LPR >= 32) v = sum_step<16>(v);
+    if constexpr (LPR >= 64) v = sum_step<32>(v);
     return v;
 }
 
+// (value, expert) pairs ordered by value, then the lower expert: a total
+// order, so the pairwise pick is symmetric and the group agrees on the top.
 template <int M>
 __device__ __forceinline__ void argmax_step(float& v, int& i) {
-    const float ov = xor_lane<M>(v);
-    const int oi = xor_lane_i32<M>(i);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    uint32_t va, vb, ia, ib;
+    lane_pair<M>(__float_as_uint(v), va, vb);
+    lane_pair<M>((uint32_t)i, ia, ib);
+    const float fa = __uint_as_float(va), fb = __uint_as_float(vb);
+    const bool take_b = (fb > fa) | ((fb == fa) & ((int)ib < (int)ia));
+    v = take_b ? fb : fa;
+    i = take_b ? (int)ib : (int)ia;
 }
 
 template <int LPR>
 __device__ __forceinline__ void group_argmax(float& v, int& i) {
-    if constexpr (LPR >= 64) argmax_step<32>(v, i);
-    if constexpr (LPR >= 32) argmax_step<16>(v, i);
-    if constexpr (LPR >= 16) argmax_step<8>(v, i);
-    if constexpr (LPR >= 8) argmax_step<4>(v, i);
-    if constexpr (LPR >= 4) argmax_step<2>(v, i);
     if constexpr (LPR >= 2) argmax_step<1>(v, i);
+    if constexpr (LPR >= 4) argmax_step<2>(v, i);
+    if constexpr (LPR >= 8) argmax_step<4>(v, i);
+    if constexpr (LPR >= 16) argmax_step<8>(v, i);
+    if constexpr (LPR >= 32) argmax_step<16>(v, i);
+    if constexpr (LPR >= 64) argmax_step<32>(v, i);
 }
 
 template <int VPT, int INDT>
@@ -92,47 +136,88 @@ __device__ __forceinline__ void load_row_values(const void* __restrict__ logits,
 // Softmax over one token's E logits held by a group of LPR lanes (lane g of
 // the group: experts e0 + q*ESTR, q < VPT, -inf past E), then the top k in
 // descending order, ties to the lower index; lane j % LPR writes output j.
-template <int VPT, int LPR, int OUTDT, int ESTR = 1>
-__device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
-                                                   long long row, bool valid, void* __restrict__ wout,
-                                                   uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout) {
-    float m = x[0];
+// R independent tokens per lane group at once (row r's logits in x[r]): their
+// cross-lane exchanges interleave, which hides the swizzle latencies when a
+// SIMD holds a single wave.
+template <int VPT, int LPR, int OUTDT, int ESTR, int R>
+__device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int e0, int g, int E, int k, int T,
+                                                  const long long (&row)[R], const bool (&valid)[R],
+                                                  void* __restrict__ wout, uint32_t* __restrict__ iout,
+                                                  uint32_t* __restrict__ eiout) {
+    float m[R];
 #pragma unroll
-    for (int j = 1; j < VPT; ++j) m = fmaxf(m, x[j]);
-    m = group_max<LPR>(m);
-
-    float p[VPT];
-    double s = 0.0;
+    for (int r = 0; r < R; ++r) {
+        m[r] = x[r][0];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const float d = x[j] - m;
-        p[j] = (e0 + j * ESTR < E) ? (float)exp((double)d) : 0.0f;
-        s += (double)p[j];
+        for (int j = 1; j < VPT; ++j) m[r] = fmaxf(m[r], x[r][j]);
     }
-    s = group_sum<LPR>(s);
-    const float S = (float)s;
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) p[j] = (e0 + j * ESTR < E) ? p[j] / S : -1.0f;
+    for (int r = 0; r < R; ++r) m[r] = group_max<LPR>(m[r]);
+
+    float p[R][VPT];
+    double s[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        s[r] = 0.0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const float d = x[r][j] - m[r];
+            p[r][j] = (e0 + j * ESTR < E) ? (float)exp((double)d) : 0.0f;
+            s[r] += (double)p[r][j];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] = group_sum<LPR>(s[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float S = (float)s[r];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) p[r][j] = (e0 + j * ESTR < E) ? p[r][j] / S : -1.0f;
+    }
 
     typedef typename Elem<OUTDT>::storage WS;
     WS* wo = reinterpret_cast<WS*>(wout);
     for (int j = 0; j < k; ++j) {
-        float bv = p[0];
-        int bi = e0;
+        float bv[R];
+        int bi[R];
 #pragma unroll
-        for (int q = 1; q < VPT; ++q)
-            if (p[q] > bv) { bv = p[q]; bi = e0 + q * ESTR; }
-        group_argmax<LPR>(bv, bi);
-        if (valid && g == (j % LPR)) {
-            const long long o = row * (long long)k + j;
-            wo[o] = Elem<OUTDT>::from_f32(bv);
-            iout[o] = (uint32_t)bi;
-            eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)row;
+        for (int r = 0; r < R; ++r) {
+            bv[r] = p[r][0];
+            bi[r] = e0;
+#pragma unroll
+            for (int q = 1; q < VPT; ++q) {
+                const bool take = p[r][q] > bv[r];
+                bv[r] = take ? p[r][q] : bv[r];
+                bi[r] = take ? e0 + q * ESTR : bi[r];
+            }
         }
 #pragma unroll
-        for (int q = 0; q < VPT; ++q)
-            if (e0 + q * ESTR == bi) p[q] = -2.0f;
+        for (int r = 0; r < R; ++r) group_argmax<LPR>(bv[r], bi[r]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int q = 0; q < VPT; ++q) p[r][q] = (e0 + q * ESTR == bi[r]) ? -2.0f : p[r][q];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (valid[r] && g == (j % LPR)) {
+                const long long o = row[r] * (long long)k + j;
+                wo[o] = Elem<OUTDT>::from_f32(bv[r]);
+                iout[o] = (uint32_t)bi[r];
+                eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)row[r];
+            }
+        }
     }
+}
+
+template <int VPT, int LPR, int OUTDT, int ESTR = 1>
+__device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
+                                                   long long row, bool valid, void* __restrict__ wout,
+                                                   uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout) {
+    const float(&xr)[1][VPT] = reinterpret_cast<const float(&)[1][VPT]>(x);
+    const long long rr[1] = {row};
+    const bool vr[1] = {valid};
+    softmax_topk_rows<VPT, LPR, OUTDT, ESTR, 1>(xr, e0, g, E, k, T, rr, vr, wout, iout, eiout);
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
@@ -318,115 +403,155 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
     softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
 }
 
-// 16-bit router on the matrix cores: one workgroup per 32 tokens, KW waves
-// splitting K (wave w takes the 32-wide chunks w, w+KW, ...), the E experts
-// padded to NB blocks of 32 columns, v_mfma_f32_32x32x16 with both operands
-// straight from global memory: the K order inside each 32-wide chunk is
-// permuted identically for x and the weight rows (lane half hh takes the 16
-// consecutive h at 16*hh, as two MFMA k16 steps), so that every lane loads 32
-// contiguous bytes of its row. The result layout puts expert 32c + l%32 of
-// token 8(i/4) + 4(l/32) + i%4 in register i of block c of lane l. The KW
-// partial sums meet in LDS (summed in wave order: deterministic); wave w then
-// takes registers i of [16w/KW, 16(w+1)/KW), each one token per 32-lane half,
-// for the softmax over 32-lane groups (VPT = NB experts per lane, stride 32).
-// Every workgroup reads the whole weight (E*H*2 bytes) once from L2, so the
-// K split (rather than fewer tokens per workgroup) is what spreads a small
-// batch over more waves.
-template <int DT, int NB, int KW, int D>
-__global__ __launch_bounds__(64 * KW) void router_mfma_kernel(const void* __restrict__ xin,
+// 16-bit router on the matrix cores (E > 32): one workgroup per 32*MT tokens
+// and NB waves, wave c computing the logits of experts 32c .. 32c+31 with
+// v_mfma_f32_32x32x16 (A = token rows, B = weight rows, both K-contiguous).
+// K tiles of 64 reach LDS by buffer_load ... lds in an NST-stage ring, each
+// instruction covering 8 rows x 128 contiguous bytes (row loads straight
+// into the MFMA fragment registers touch 32 rows per instruction, which the
+// address unit serialises); rows past T or E and the K tail read as zeros.
+// Rows of a stage hold 8 16-byte chunks, chunk c of row r at a_swz(r, c)
+// (conflict-free fragment reads). The result layout puts expert 32c + l%32
+// of token 32m + 8(i/4) + 4(l/32) + i%4 in register i of block m of lane l;
+// the waves swap blocks through LDS so that each holds whole tokens for the
+// softmax over 32-lane groups (VPT = NB experts per lane, stride 32).
+template <int DT, int NB, int MT, int NST>
+__global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __restrict__ xin,
                                                               const void* __restrict__ win,
                                                               float* __restrict__ wout, uint32_t* __restrict__ iout,
                                                               uint32_t* __restrict__ eiout, int T, int H, int E,
                                                               int k) {
-    static_assert(KW == 4 || KW == 8, "waves");
+    using namespace lds;
     typedef typename Elem<DT>::storage S;
-    __shared__ float red[KW][NB][16][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const long long t0 = (long long)blockIdx.x * 32;  // < T (grid = ceil(T/32))
-    const int r = lane & 31, hh = lane >> 5;
-    const long long xrow = t0 + r < T ? t0 + r : (long long)T - 1;  // rows past T compute garbage, unused
-    const S* xr = reinterpret_cast<const S*>(xin) + xrow * H + 16 * hh;
-    const S* wr[NB];
+    constexpr int TM = 32 * MT;                   // tokens per workgroup
+    constexpr int EW = 32 * NB;                   // weight rows (experts, padded)
+    constexpr int STAGE = (TM + EW) * 128;        // one K tile of 64: 128 bytes per row
+    constexpr int INS = STAGE / 1024;             // DMA instructions per stage (8 rows each)
+    constexpr int LOADS = INS / NB;               // per wave
+    static_assert(LOADS * NB == INS && LOADS * (NST - 2) < 64, "router stage split");
+    static_assert(MT * NB * 16 * 64 * 4 <= NST * STAGE, "softmax exchange fits the ring");
+    __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long long t0 = (long long)blockIdx.x * TM;  // < T (grid = ceil(T/TM))
+    const int rows = T - t0 < TM ? (int)(T - t0) : TM;
+    const i32x4 rx = make_rsrc(reinterpret_cast<const S*>(xin) + t0 * H, (long long)rows * H * 2);
+    const i32x4 rw = make_rsrc(win, (long long)E * H * 2);
+    const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+
+    // per-lane source offsets of this wave's LOADS instructions (instruction
+    // q = NB*i + wave of the stage: rows 8q .. 8q+7, token rows first), the K
+    // position of a full tile in the SGPR offset
+    uint32_t off[LOADS];
+    int chunk_k[LOADS];
+    bool is_x[LOADS];
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
-        wr[c] = reinterpret_cast<const S*>(win) + (long long)(r + 32 * c < E ? r + 32 * c : 0) * H + 16 * hh;
-    f32x16 acc[NB];
+    for (int i = 0; i < LOADS; ++i) {
+        const int q = NB * i + wave;
+        const int row = 8 * q + lane / 8;  // row of the stage
+        const int c = a_swz<8>(row, lane % 8);
+        chunk_k[i] = 8 * c;
+        is_x[i] = 8 * q < TM;  // whole instructions: TM is a multiple of 8 (wave-uniform)
+        off[i] = is_x[i] ? ((uint32_t)row * (uint32_t)H + 8u * c) * 2u
+                         : ((uint32_t)(row - TM) * (uint32_t)H + 8u * c) * 2u;  // rows >= rows / E: past the resource
+    }
+    const int nk = (H + 63) / 64;
+    auto issue = [&](int stage, int k0) {
+        const uint32_t sl = sbase + stage * STAGE;
+        const bool full = k0 + 64 <= H;
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[c][i] = 0.f;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    // D of this wave's chunks in flight: the loads of its chunk j + D are
-    // issued as chunk j is consumed (slot = j % D, unrolled so slots are
-    // registers)
-    u32x4 xa[D][2], wb[D][NB][2];
-    auto load = [&](int sl, int j) {
-        const int k0 = (wave + KW * j) * 32;
-        const bool in0 = k0 + 16 * hh < H, in1 = k0 + 16 * hh + 8 < H;
-        xa[sl][0] = in0 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0)) : z;
-        xa[sl][1] = in1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + k0 + 8)) : z;
-#pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            const bool ev = r + 32 * c < E;
-            wb[sl][c][0] = (ev && in0) ? *reinterpret_cast<const u32x4*>(wr[c] + k0) : z;
-            wb[sl][c][1] = (ev && in1) ? *reinterpret_cast<const u32x4*>(wr[c] + k0 + 8) : z;
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t v = (full || k0 + chunk_k[i] < H) ? off[i] : kOob;
+            dma16s(is_x[i] ? rx : rw, sl + (NB * i + wave) * 1024, v, (uint32_t)k0 * 2u);
         }
     };
-    const int nch = (H + 31) / 32;
-    const int mine = nch > wave ? (nch - wave + KW - 1) / KW : 0;  // this wave's chunks
+
+    f32x16 acc[MT];
 #pragma unroll
-    for (int sl = 0; sl < D; ++sl)
-        if (sl < mine) load(sl, sl);
-    for (int j0 = 0; j0 < mine; j0 += D) {
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int sl = 0; sl < D; ++sl) {
-            if (j0 + sl < mine) {
+        for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+    const int lr = lane & 31, lh = lane >> 5;
 #pragma unroll
-                for (int c = 0; c < NB; ++c) {
-                    acc[c] = mfma32<DT>(xa[sl][0], wb[sl][c][0], acc[c]);
-                    acc[c] = mfma32<DT>(xa[sl][1], wb[sl][c][1], acc[c]);
-                }
-                if (j0 + sl + D < mine) load(sl, j0 + sl + D);
+    for (int s = 0; s < NST - 1; ++s)
+        if (s < nk) issue(s, s * 64);
+    for (int kt = 0; kt < nk; ++kt) {
+        // this wave's DMA of tile kt (NST-2 newer tiles may stay in flight),
+        // then the barrier makes every wave's part visible and frees slot kt-1
+        const int newer = min(NST - 2, nk - 1 - kt);
+        if (newer >= 4) wait_vm<4 * LOADS>();
+        else if (newer == 3) wait_vm<3 * LOADS>();
+        else if (newer == 2) wait_vm<2 * LOADS>();
+        else if (newer == 1) wait_vm<LOADS>();
+        else wait_vm<0>();
+        wait_lgkm0();
+        block_barrier();
+        if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt + NST - 1) * 64);
+        const char* sx = smem + (kt % NST) * STAGE;
+        const char* sw = sx + TM * 128;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int c = 2 * st + lh;
+            const int wr = 32 * wave + lr;  // weight row; stage row TM + wr (the swizzle's row)
+            const u32x4 b = *reinterpret_cast<const u32x4*>(sw + wr * 128 + a_swz<8>(TM + wr, c) * 16);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int xr = 32 * m + lr;
+                const u32x4 a = *reinterpret_cast<const u32x4*>(sx + xr * 128 + a_swz<8>(xr, c) * 16);
+                acc[m] = mfma32<DT>(a, b, acc[m]);
             }
         }
     }
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) red[wave][c][i][lane] = acc[c][i];
+    // exchange through LDS (the ring is free after the barrier): red[m][c][i][lane]
+    wait_lgkm0();
     __syncthreads();
-    constexpr int RPW = 16 / KW;  // result registers per wave
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[((m * NB + wave) * 16 + i) * 64 + lane] = acc[m][i];
+    __syncthreads();
+    // wave w takes result registers g = NB*ii + w ((m, i) = (g / 16, g % 16)):
+    // the first tokens spread over all waves when the batch is small
+    constexpr int RPW = MT * 16 / NB;  // result registers per wave
+    static_assert(RPW * NB == MT * 16, "register split");
+    float x[RPW][NB];
+    long long row[RPW];
+    bool valid[RPW];
 #pragma unroll
     for (int ii = 0; ii < RPW; ++ii) {
-        const int i = RPW * wave + ii;
-        const long long row = t0 + 8 * (i / 4) + 4 * hh + (i % 4);
-        const bool valid = row < T;
-        float x[NB];
+        const int g = NB * ii + wave;
+        const int m = g / 16, i = g % 16;
+        const long long rw_ = t0 + 32 * m + 8 * (i / 4) + 4 * lh + (i % 4);
+        valid[ii] = rw_ < T;
+        row[ii] = valid[ii] ? rw_ : 0;
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
-            float sum = red[0][c][i][lane];
-#pragma unroll
-            for (int w = 1; w < KW; ++w) sum += red[w][c][i][lane];
+            const float v = red[((m * NB + c) * 16 + i) * 64 + lane];
             // the logit as the matmul would store it in the input dtype
-            x[c] = r + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(sum)) : -__builtin_inff();
+            x[ii][c] = lr + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(v)) : -__builtin_inff();
         }
-        softmax_topk_group<NB, 32, kF32, 32>(x, r, r, E, k, T, valid ? row : 0, valid, wout, iout, eiout);
     }
+    softmax_topk_rows<NB, 32, kF32, 32, RPW>(x, lr, lr, E, k, T, row, valid, wout, iout, eiout);
 }
 
 template <int DT, int NB>
 static hipError_t launch_router_mfma(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                      int H, int E, int k, hipStream_t stream) {
-    const long long grid = ((long long)T + 31) / 32;
-    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-    // fewer workgroups than CUs: 8 waves per workgroup, otherwise 4
-    constexpr int D = NB == 2 ? 4 : 3;
-    if (grid < 256)
-        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 8, D>), dim3((unsigned)grid), dim3(512), 0, stream, x, w, wo,
-                           io, eo, T, H, E, k);
-    else
-        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 4, D>), dim3((unsigned)grid), dim3(256), 0, stream, x, w, wo,
-                           io, eo, T, H, E, k);
+    // 64 tokens per workgroup (each weight tile serves twice the rows) once
+    // that still gives >= 256 workgroups, 3 stages (72 KB: two workgroups per
+    // CU, 85 -> 63 us at T=32768, E=128 against 5 stages); else 32 tokens and
+    // 6 stages (the one workgroup of a CU keeps more of the weight in flight)
+    if ((long long)T >= 256LL * 64) {
+        const long long grid = ((long long)T + 63) / 64;
+        if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 2, 3>), dim3((unsigned)grid), dim3(64 * NB), 0, stream, x, w,
+                           wo, io, eo, T, H, E, k);
+    } else {
+        const long long grid = ((long long)T + 31) / 32;
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 1, 6>), dim3((unsigned)grid), dim3(64 * NB), 0, stream, x, w,
+                           wo, io, eo, T, H, E, k);
+    }
     return hipGetLastError();
 }
 

@@ -158,7 +158,7 @@ int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_d
  *   then topk_softmax of f32(logits): topk_weight f32 [T,k], topk_indices u32 [T,k],
  *   token_expert_indices u32 [T,k] = j*T + t.
  *   hidden [T,H], router_weight [E,H] (candle Linear layout), both `dtype`,
- *   16-byte aligned; H a multiple of 8 (4 for f32); 1 <= E <= 128.
+ *   16-byte aligned; H a multiple of 8 (4 for f32), at most 2^22; 1 <= E <= 128.
  * Reads hidden once (HBM-bound); the logits never reach memory. */
 int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight,
                            void* topk_indices, void* token_expert_indices, int num_tokens,

@@ -115,4 +115,6 @@ def test_router_topk_errors():
     xo = ctypes.c_void_p(x.data_ptr() + 2)
     assert L.candle_moe_router_topk(xo, p(w), p(out), p(idx), p(idx), 2, 64, 8, 2, O.BF16, s) != 0
     assert "aligned" in candle_moe.last_error()
+    assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 4, (1 << 22) + 8, 8, 2, O.BF16, s) != 0
+    assert "4194304" in candle_moe.last_error()
     assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 0, 64, 8, 2, O.BF16, s) == 0
