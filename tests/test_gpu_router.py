@@ -47,9 +47,10 @@ def quantized(shape, denom, seed):
 @pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
 @pytest.mark.parametrize("T,H,E,k", [(1000, 4096, 8, 2), (333, 768, 8, 2), (129, 2048, 128, 8), (77, 1024, 64, 6),
                                      (50, 512, 16, 4), (40, 256, 32, 3), (9, 64, 5, 5),
-                                     # 16-bit E > 32 (matrix cores): 8 waves per workgroup below 256
-                                     # workgroups of 32 tokens, 4 from there; H not a multiple of 32
-                                     (8200, 512, 128, 8), (8200, 1000, 40, 3), (300, 1000, 96, 4), (1, 2048, 128, 8)])
+                                     # 16-bit E > 32 (matrix cores): 32 tokens per workgroup below
+                                     # 16384 tokens, 64 from there; H tails inside a K tile of 64
+                                     (8200, 512, 128, 8), (8200, 1000, 40, 3), (300, 1000, 96, 4), (1, 2048, 128, 8),
+                                     (16400, 256, 128, 8), (16400, 264, 40, 2)])
 def test_router_topk_exact(dt, T, H, E, k):
     x = O.to_dtype(quantized((T, H), 8.0, T + H), dt)
     w = O.to_dtype(quantized((E, H), 64.0, E + k), dt)
