@@ -94,33 +94,58 @@ __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
             s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
 }
 
-// Exclusive scan of v[0..n) in place (one workgroup of kGroupThreads),
-// returning the total; s_part is kGroupThreads ints of scratch. Each thread
-// scans a contiguous run of ceil(n / threads) entries.
-__device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* s_part) {
+// Exclusive scans of u[0..n) and v[0..n) in place (one workgroup of
+// kGroupThreads), returning the totals; s_part is 8 ints of scratch. Each
+// thread scans a contiguous run of ceil(n / threads) entries of both; the
+// per-thread sums are scanned inside each wave by shuffles and across the 4
+// waves through LDS (two barriers).
+__device__ void block_exclusive_scan2(int32_t* u, int32_t* v, int n, int32_t* s_part, int32_t& total_u,
+                                      int32_t& total_v) {
+    constexpr int NW = kGroupThreads / 64;
     const int per = (n + kGroupThreads - 1) / kGroupThreads;
     const int lo = threadIdx.x * per;
     const int hi = lo + per < n ? lo + per : n;
-    int32_t run = 0;
-    for (int i = lo; i < hi; ++i) run += v[i];
-    s_part[threadIdx.x] = run;
-    __syncthreads();
-    // Hillis-Steele over the per-thread sums
-    for (int d = 1; d < kGroupThreads; d <<= 1) {
-        const int32_t add = threadIdx.x >= d ? s_part[threadIdx.x - d] : 0;
-        __syncthreads();
-        s_part[threadIdx.x] += add;
-        __syncthreads();
-    }
-    const int32_t total = s_part[kGroupThreads - 1];
-    int32_t base = s_part[threadIdx.x] - run;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int32_t ru = 0, rv = 0;
     for (int i = lo; i < hi; ++i) {
-        const int32_t c = v[i];
-        v[i] = base;
-        base += c;
+        ru += u[i];
+        rv += v[i];
+    }
+    int32_t iu = ru, iv = rv;  // inclusive within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t tu = __shfl_up(iu, d), tv = __shfl_up(iv, d);
+        if (lane >= d) {
+            iu += tu;
+            iv += tv;
+        }
+    }
+    if (lane == 63) {
+        s_part[wave] = iu;
+        s_part[NW + wave] = iv;
     }
     __syncthreads();
-    return total;
+    int32_t bu = iu - ru, bv = iv - rv;
+    total_u = 0;
+    total_v = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const int32_t wu = s_part[w], wv = s_part[NW + w];
+        if (w < wave) {
+            bu += wu;
+            bv += wv;
+        }
+        total_u += wu;
+        total_v += wv;
+    }
+    for (int i = lo; i < hi; ++i) {
+        const int32_t cu = u[i], cv = v[i];
+        u[i] = bu;
+        v[i] = bv;
+        bu += cu;
+        bv += cv;
+    }
+    __syncthreads();
 }
 
 // One workgroup. block_counts[b][e] becomes the number of bin-e items in
@@ -193,8 +218,8 @@ __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
     if (staged)
         for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) block_counts[i] = s_bc[i];
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) atomicMax(&s_max, s_tot[e]);
-    const int32_t total = block_exclusive_scan(s_tot, nbins, s_part);
-    const int32_t tiles = block_exclusive_scan(s_tb, nbins, s_part);
+    int32_t total, tiles;
+    block_exclusive_scan2(s_tot, s_tb, nbins, s_part, total, tiles);
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
         offsets[e] = s_tot[e];
         const int32_t c = (e + 1 < nbins ? s_tot[e + 1] : total) - s_tot[e];
@@ -285,12 +310,18 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
     }
 }
 
-// All of grouping in one workgroup, for at most kGroupSmallMax items: LDS
-// histogram, block-wide scans of the counts and of the per-bin tile counts,
-// the tile table, and the stable ballot scatter. Also clears zero_n ints at
-// zero_ptr (the split-K arrival counters of the GEMMs that follow).
+// All of grouping in one workgroup, for at most kGroupSmallMax items. Wave w
+// takes items [w*64*IPT, (w+1)*64*IPT), 64 at a time, reads their bins once
+// (all loads in flight together) and ranks them stably as the scatter phase
+// does (ballot peer masks, per-wave running counts in LDS); the per-wave
+// counts give the bin totals, whose scans give the offsets and the tile
+// table, and then per-wave bases, so each item goes to base + its rank. Also
+// clears zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs
+// that follow).
 template <bool TOK>
 __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
+    constexpr int NW = kGroupThreads / 64;
+    constexpr int IPT = kGroupSmallMax / kGroupThreads;  // items per lane
     const uint32_t* __restrict__ idx = j.idx;
     const int P = (int)j.items, k = j.k, E = j.E, nbins = j.nbins, ebits = j.ebits, BM = j.BM;
     int32_t* __restrict__ offsets = j.b.offsets;
@@ -301,32 +332,57 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
     int32_t* __restrict__ pair_dest = j.pair_dest;
     int32_t* __restrict__ zero_ptr = j.b.zero_ptr;
     const int zero_n = j.b.zero_n;
-    int32_t* s_cnt = s_mem;               // [4][nbins] per-wave histogram, then per-wave step counts
-    int32_t* s_off = s_mem + 4 * nbins;   // [nbins] bin offsets -> running positions
-    int32_t* s_tb = s_off + nbins;        // [nbins] tile bases
-    int32_t* s_part = s_tb + nbins;       // [kGroupThreads] scan scratch
+    int32_t* s_cnt = s_mem;               // [NW][nbins] per-wave counts, then per-wave bases
+    int32_t* s_off = s_mem + NW * nbins;  // [nbins] bin totals -> offsets
+    int32_t* s_tb = s_off + nbins;        // [nbins] tile counts -> tile bases
+    int32_t* s_part = s_tb + nbins;       // scan scratch
     __shared__ int32_t s_max;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wbase = wave * 64 * IPT;
+    int bin[IPT], lrank[IPT];
+    int rank[kSetMaxK];
+    // the bins first: the loads of all IPT items are in flight together
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        const int p = wbase + s * 64 + lane;
+        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+    }
     for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
-    for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
+    for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_cnt[i] = 0;
     if (threadIdx.x == 0) s_max = 0;
     __syncthreads();
-    int rank[kSetMaxK];
-    for (int p = threadIdx.x; p < P; p += kGroupThreads) {
-        const int b = item_bin<TOK>(idx, p, k, E, rank);
-        if (b >= 0) atomicAdd(s_cnt + wave * nbins + b, 1);
+    int32_t* mine = s_cnt + wave * nbins;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        if (wbase + s * 64 >= P) break;  // wave-uniform
+        const int b = bin[s];
+        const bool active = b >= 0;
+        const uint32_t e = active ? (uint32_t)b : 0xffffffffu;
+        uint64_t peers = __ballot(active);
+        for (int i = 0; i < ebits; ++i) {
+            const bool bit = (e >> i) & 1u;
+            const uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        const int r = __popcll(peers & lt_mask);
+        // every lane reads the running count before the bin's first lane
+        // stores the new one (LDS instructions of a wave execute in order)
+        const int before = active ? mine[b] : 0;
+        if (active && r == 0) mine[b] = before + __popcll(peers);
+        lrank[s] = before + r;
     }
     __syncthreads();
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
-        const int32_t c = s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
+        int32_t c = 0;
+        for (int w = 0; w < NW; ++w) c += s_cnt[w * nbins + e];
         s_off[e] = c;
         s_tb[e] = (c + BM - 1) / BM;
         atomicMax(&s_max, c);
-        s_cnt[e] = s_cnt[nbins + e] = s_cnt[2 * nbins + e] = s_cnt[3 * nbins + e] = 0;
     }
     __syncthreads();
-    const int32_t total = block_exclusive_scan(s_off, nbins, s_part);
-    const int32_t tiles = block_exclusive_scan(s_tb, nbins, s_part);
+    int32_t total, tiles;
+    block_exclusive_scan2(s_off, s_tb, nbins, s_part, total, tiles);
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
         offsets[e] = s_off[e];
         const int32_t c = (e + 1 < nbins ? s_off[e + 1] : total) - s_off[e];
@@ -335,6 +391,13 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
             tile_row[s_tb[e] + i] = s_off[e] + i * BM;
             tile_exp[s_tb[e] + i] = e;
         }
+        // per-wave bases of bin e: its offset plus the counts of earlier waves
+        int32_t run = s_off[e];
+        for (int w = 0; w < NW; ++w) {
+            const int32_t t = s_cnt[w * nbins + e];
+            s_cnt[w * nbins + e] = run;
+            run += t;
+        }
     }
     if (threadIdx.x == 0) {
         offsets[nbins] = total;
@@ -342,36 +405,16 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
         *num_tiles = tiles;
     }
     __syncthreads();
-    // stable scatter: s_off[e] is the next free position of bin e
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int s0 = 0; s0 < P; s0 += kGroupThreads) {
-        const int p = s0 + threadIdx.x;
-        const int bin = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
-        const bool active = bin >= 0;
-        const uint32_t e = active ? (uint32_t)bin : 0xffffffffu;
-        uint64_t peers = __ballot(active);
-        for (int b = 0; b < ebits; ++b) {
-            const bool bit = (e >> b) & 1u;
-            const uint64_t bal = __ballot(bit);
-            peers &= bit ? bal : ~bal;
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        if (bin[s] < 0) continue;
+        const int p = wbase + s * 64 + lane;
+        const int32_t pos = mine[bin[s]] + lrank[s];
+        sorted_pair[pos] = p;
+        if constexpr (TOK) {
+            (void)token_set_key(idx, p, k, E, rank);
+            for (int jj = 0; jj < k; ++jj) pair_dest[(long long)p * k + jj] = pos * k + rank[jj];
         }
-        const int lrank = __popcll(peers & lt_mask);
-        if (active && lrank == 0) s_cnt[wave * nbins + e] = __popcll(peers);
-        __syncthreads();
-        if (active) {
-            int32_t pos = s_off[e] + lrank;
-            for (int w = 0; w < wave; ++w) pos += s_cnt[w * nbins + e];
-            sorted_pair[pos] = p;
-            if constexpr (TOK) {
-                for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
-            }
-        }
-        __syncthreads();
-        for (int ee = threadIdx.x; ee < nbins; ee += kGroupThreads) {
-            s_off[ee] += s_cnt[ee] + s_cnt[nbins + ee] + s_cnt[2 * nbins + ee] + s_cnt[3 * nbins + ee];
-            s_cnt[ee] = s_cnt[nbins + ee] = s_cnt[2 * nbins + ee] = s_cnt[3 * nbins + ee] = 0;
-        }
-        __syncthreads();
     }
 }
 
