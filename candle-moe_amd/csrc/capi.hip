@@ -135,6 +135,7 @@ struct Problem {
     bool lds_family;  // both GEMMs run moe_lds_gemm (fused clears and K splits available)
     bool fused_clear_ok;  // the gate/up kernel can clear the pair path's accumulator
     int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
+    int split_target; // K splits: the kernels aim at this many workgroups (live tiles * splits)
 };
 
 // CUs per XCD of the current device (its CUs over the 8 XCDs of MI355X), 0
@@ -205,11 +206,13 @@ static Layout make_layout(const Problem& p) {
     // one after the other; the counters are left zero)
     L.partial = L.counters = o;
     if (p.split1 > 1 || p.split2 > 1) {
-        const size_t t1 = (size_t)mt * p.n_tiles1 * (p.split1 > 1 ? p.split1 : 0);
-        const size_t t2 = (size_t)mt * p.n_tiles2 * (p.split2 > 1 ? p.split2 : 0);
+        // partial slots: live tiles * splits, at most split_target with the
+        // device's choice, else the host's fixed split over the most tiles
         const size_t c1 = p.split1 > 1 ? (size_t)mt * p.n_tiles1 : 0;
         const size_t c2 = p.split2 > 1 ? (size_t)mt * p.n_tiles2 : 0;
-        L.partial = o; o += a256((t1 > t2 ? t1 : t2) * p.BM * tile_cols(p.cfg) * 4);
+        const size_t slots = p.split_target > 0 ? (size_t)p.split_target
+                                                : std::max(c1 * p.split1, c2 * p.split2);
+        L.partial = o; o += a256(slots * p.BM * tile_cols(p.cfg) * 4);
         L.counters = o; o += a256((c1 > c2 ? c1 : c2) * 4);
     } else if (p.tail_cus > 0) {
         const size_t slots = 8 * (size_t)p.tail_cus;
@@ -291,12 +294,19 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= 0.5 * p.BM * sets);
         }
     }
-    // K splits for the 32-row (decode) GEMMs whose expected output tiles
-    // (< 128) leave most CUs idle: up to ~256 workgroups, at most 8 splits,
-    // no empty split; for the f32 kernels (< 256 tiles) up to ~512
-    // workgroups and 16 splits. Each split writes an f32 partial tile that
-    // the last one sums, so splitting only pays where the weight stream would
-    // otherwise run on a few CUs.
+    // K splits for the 32-row (decode) GEMMs and the f32 kernels, whose output
+    // tiles can leave most CUs idle. Each split writes an f32 partial tile
+    // that the last one sums, so splitting only pays where the weight stream
+    // would otherwise run on a few CUs.
+    //  * 32-row MFMA kernels: the kernel picks the count from the live tiles of
+    //    the grouping (adaptive_split): one round of workgroups (one per CU),
+    //    at most 8 splits; here only the bound and the target. (A second round
+    //    measured slower: Qwen3 T=64 gate/up 52 -> 47 us, Qwen3-30B-A3B T=1
+    //    25 -> 20 us against the host's estimate.)
+    //  * f32 kernels (two workgroups per CU, one K chunk in flight each): the
+    //    host's count from the expected tiles, up to ~512 workgroups and 16
+    //    splits (they gain from more than one round: Nomic T=512 f32 fc1
+    //    136 us against 150-190 us with the device's one-round choice).
     p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
     p.fused_clear_ok = p.lds_family || is_f32_cfg(p.cfg);
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
@@ -306,13 +316,17 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // split-K fixup): the tiles of each XCD's last, partly filled round are
     // split along K
     p.tail_cus = (p.lds_family && p.cfg == kLds256w8) ? cus_per_xcd() : 0;
-    if (((p.lds_family && p.cfg == kLdsRows32) || is_f32_cfg(p.cfg)) && P > 0) {
+    p.split_target = 0;
+    if (p.lds_family && p.cfg == kLdsRows32 && P > 0) {
+        p.split_target = cus_per_xcd() > 0 ? 8 * cus_per_xcd() : 256;
+        const int bk = tile_bk(p.cfg);
+        auto bound = [&](int K) { return std::max(1, std::min(8, cdiv(K, bk))); };
+        if (!p.set_path) p.split2 = bound(I);
+        p.split1 = bound(H);
+    } else if (is_f32_cfg(p.cfg) && P > 0) {
         const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);
-        // the f32 kernel keeps one K chunk in flight per workgroup: twice the
-        // workgroups, up to 16 splits (both tile heights)
-        const bool f32 = is_f32_cfg(p.cfg);
-        const long long target = f32 ? 512 : 256, max_sp = f32 ? 16 : 8;
+        const long long target = 512, max_sp = 16;
         auto choose = [&](long long tiles, int K) {
             if (tiles >= target / 2) return 1;
             const int nk = (K + bk - 1) / bk;
@@ -396,6 +410,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.n_tiles = p.n_tiles1;
     g1.m_tiles_max = m_tiles_max;
     g1.ksplit = p.split1;
+    g1.split_target = p.split_target;
     g1.partial = reinterpret_cast<float*>(ws + L.partial);
     g1.counters = counters;
     g1.tail_cus = p.tail_cus;
@@ -469,6 +484,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     const int mode2 = qwen3 ? kDown : kFc2;
     g2.n_tiles = p.n_tiles2;
     g2.ksplit = p.split2;
+    g2.split_target = p.split_target;
     g2.partial = reinterpret_cast<float*>(ws + L.partial);
     g2.counters = counters;
     g2.zero_f32 = nullptr;

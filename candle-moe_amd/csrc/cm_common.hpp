@@ -150,6 +150,22 @@ __device__ __forceinline__ int xcd_logical(int live) {
     return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 
+// K splits of a launch with `live` output tiles (known on the device only,
+// from the grouping): target / live, target = workgroups that fill the
+// device once, so live * splits <= target (one round of workgroups: the
+// weight-streaming 32-row kernels gain nothing from a second); at most
+// max_split, no empty split among nk K tiles. target <= 0: max_split as
+// given (fixed by the host).
+__device__ __forceinline__ int adaptive_split(int max_split, int target, int live, int nk) {
+    if (max_split <= 1) return 1;
+    if (target <= 0) return max_split;
+    int sp = live > 0 ? target / live : max_split;
+    sp = sp < 1 ? 1 : (sp > max_split ? max_split : sp);
+    sp = sp < nk ? sp : (nk > 0 ? nk : 1);
+    const int per = (nk + sp - 1) / sp;
+    return per > 0 ? (nk + per - 1) / per : 1;
+}
+
 // Output tile (row tile mt, column tile nt) of this workgroup, or false when
 // it has none: the row-tile count m_live comes from the grouping on the device.
 __device__ __forceinline__ bool tile_coords(int n_tiles, int m_live, int& mt, int& nt) {

@@ -94,8 +94,10 @@ struct GemmArgs {
     int seg_len;              // set GEMM2: K length of one slot's segment (= I)
     long long a_bytes;        // size of A in bytes (LDS-DMA kernels: buffer range, < 2^31)
     // split-K and fused clears (moe_lds_gemm only)
-    int ksplit;               // workgroups per output tile along K (<= 1: one)
-    float* partial;           // non-atomic modes with ksplit > 1: [m_tiles_max*n_tiles][ksplit][BM*BN] f32
+    int ksplit;               // most workgroups per output tile along K (<= 1: one)
+    int split_target;         // > 0: the kernel takes ~split_target / live tiles splits (at most
+                              // ksplit; adaptive_split); 0: ksplit
+    float* partial;           // ksplit > 1: [tile * splits + split][BM*BN] f32 slots
     int32_t* counters;        // [m_tiles_max*n_tiles] arrival counters: zero on entry, left zero
     float* zero_f32;          // f32 range cleared by this launch's workgroups (null: none)
     long long zero_n;
@@ -142,6 +144,13 @@ inline int tile_cols(int cfg) {
                                                                                                                     : 256);
 }
 inline bool is_lds_cfg(int cfg) { return cfg >= kLds256 && !is_f32_cfg(cfg); }
+// Workgroups of a launch over at most `tiles` output tiles: with adaptive K
+// splits live tiles * splits stays within split_target when it splits.
+inline long long split_grid(long long tiles, const GemmArgs& a) {
+    if (a.ksplit <= 1) return tiles;
+    if (a.split_target <= 0) return tiles * a.ksplit;
+    return tiles > a.split_target ? tiles : a.split_target;
+}
 // K tile of the LDS-DMA kernels
 inline int tile_bk(int cfg) {
     if (is_f32_cfg(cfg)) return 16;

@@ -50,8 +50,9 @@ __global__ __launch_bounds__(256, 2) void moe_f32_gemm(GemmArgs a) {
     __shared__ int s_last;
 
     clear_share(a.zero_f32, a.zero_n);
-    const int nsplit = a.ksplit > 1 ? a.ksplit : 1;
-    const int lg = xcd_logical(*a.num_tiles * a.n_tiles * nsplit);
+    const int live = *a.num_tiles * a.n_tiles;
+    const int nsplit = adaptive_split(a.ksplit, a.split_target, live, (a.K + TK - 1) / TK);
+    const int lg = xcd_logical(live * nsplit);
     if (lg < 0) return;
     const int tile = lg / nsplit, ks = lg - tile * nsplit;
     const int mt = tile / a.n_tiles, nt = tile - mt * a.n_tiles;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void moe_f32_gemm(GemmArgs a) {
 
 template <int MODE>
 static hipError_t launch_f32_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
-    const long long nwg_l = (long long)a.m_tiles_max * a.n_tiles * (a.ksplit > 1 ? a.ksplit : 1);
+    const long long nwg_l = split_grid((long long)a.m_tiles_max * a.n_tiles, a);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     const int nwg = (int)nwg_l;
     if (nwg <= 0) return hipSuccess;

@@ -85,8 +85,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                        fix_ctr))
             return;
     } else {
-        nsplit = a.ksplit > 1 ? a.ksplit : 1;
-        const int lg = xcd_logical(*a.num_tiles * a.n_tiles * nsplit);
+        const int live = *a.num_tiles * a.n_tiles;
+        nsplit = adaptive_split(a.ksplit, a.split_target, live, (a.K + BK - 1) / BK);
+        const int lg = xcd_logical(live * nsplit);
         if (lg < 0) return;
         tile = lg / nsplit;
         ks = lg - tile * nsplit;
@@ -497,7 +498,7 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     // tail balance: each XCD's range plus up to tail_cus split workgroups
     const long long tiles = (long long)a.m_tiles_max * a.n_tiles;
     const long long nwg_l = a.tail_cus > 0 ? 8 * ((tiles + 7) / 8 + a.tail_cus)
-                                           : tiles * (a.ksplit > 1 ? a.ksplit : 1);
+                                           : split_grid(tiles, a);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     const int nwg = (int)nwg_l;
     if (nwg <= 0) return hipSuccess;
