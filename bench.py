@@ -58,6 +58,8 @@ def parse():
                     help="GEMM kernel: 0 auto, 1/2 register-staged 128/256, 3-8, 10, 11 LDS-DMA variants, 9 ping-pong, "
                          "12 32-row (decode), 13/14 256x128 / 128x256 two workgroups per CU, 15/16 f32 32-row / 128-row")
     ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the warmup, run 3 plain copy kernels of MIB MiB (read MIB, write MIB; "
                          "the reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -166,6 +168,32 @@ def main():
     kernels["gemm_gate_up"] = timed.get("gemm_gate_up", kernels.get("gemm_gate_up", 0.0))
 
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
+    graph_ms = None
+    if args.graph:
+        # capture stream warmed first (the library's workspace is per stream);
+        # the last replay is checked against an eager step
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            gout = step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        g0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - g0) * 1000.0 / args.steps
+        ref = step().float()
+        torch.cuda.synchronize()
+        rms = float(ref.pow(2).mean().sqrt())
+        if not torch.allclose(gout.float(), ref, rtol=2e-2, atol=2e-2 * rms):
+            graph_ms = None
     c = 6 if qwen3 else 4
     flops = float(T) * k * c * H * I
     tflops = flops / (ms_per_step * 1e-3) / 1e12
@@ -207,6 +235,7 @@ def main():
         "topk_softmax_us": topk_us,
         "topk_softmax_gbs": round(topk_bytes / (topk_us * 1e-6) / 1e9, 1) if topk_us else None,
         "kernels_us": kernels,
+        "graph_ms_per_step": round(graph_ms, 4) if graph_ms else None,
         "kernels_note": "HIP-event averages per launch: gemm_gate_up from the timed steps (the only kernel "
                         "bracketed there), the others from an untimed pass of up to 10 steps with every "
                         "launch bracketed",

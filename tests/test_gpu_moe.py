@@ -370,3 +370,55 @@ def test_tile_configs(tile, combine):
     finally:
         candle_moe.set_tile_policy(0)
         candle_moe.set_combine_policy(0)
+
+
+@pytest.mark.parametrize("T", [8, 1024])
+def test_step_replayed_from_a_cuda_graph(T):
+    """topk_softmax + FusedMoE.forward captured once in a torch CUDA graph (a
+    HIP graph) and replayed: the library allocates nothing once its per-stream
+    workspace exists (the capture stream is warmed eagerly first) and makes no
+    host synchronisation, so the step captures; every replay equals the eager
+    result bit for bit (k = 2: deterministic), with eager work of the same
+    library on another stream between the replays, and the eager result
+    itself matches the oracle."""
+    import torch
+
+    H, I, E, k, dt = 512, 256, 8, 2, O.BF16
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, 5, O.QWEN3)
+    logits = torch.from_numpy(O.randn((T, E), seed=6, stream=1)).to("cuda:0")
+    tx, tg, tu, td = to_dev(x, dt), to_dev(G, dt), to_dev(U, dt), to_dev(D, dt)
+    tw = torch.empty((T, k), dtype=torch.float32, device="cuda:0")
+    ti = torch.empty((T, k), dtype=torch.int32, device="cuda:0")
+    te = torch.empty((T, k), dtype=torch.int32, device="cuda:0")
+    moe = candle_moe.FusedMoE.new(E, k, candle_moe.Activation.Silu)
+
+    def step():
+        candle_moe.apply_topk_softmax_inplace(logits, tw, ti, te)
+        return moe.forward(tx, tg, tu, td, tw, ti, 0)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ref = step().clone()
+        ref_w, ref_i = tw.clone(), ti.clone()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    want = O.fused_moe(x, G, U, D, from_dev(ref_w), from_dev(ref_i).astype(np.uint32), E=E, k=k, act=O.SILU,
+                       moe_type=O.QWEN3, dtype=dt, mode=O.MODE_F32ACC)
+    assert_close(from_dev(ref).astype(np.float64), want, RTOL[dt], "eager step")
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        out = step()
+    other_w = torch.from_numpy(rw).to("cuda:0")
+    other_i = torch.from_numpy(ri.astype(np.int32)).to("cuda:0")
+    for _ in range(3):
+        eager = moe.forward(tx, tg, tu, td, other_w, other_i, 0)  # default stream, its own workspace
+        torch.cuda.synchronize()
+        out.zero_()
+        tw.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert torch.equal(tw, ref_w) and torch.equal(ti, ref_i)
+        assert torch.isfinite(eager.float()).all()
