@@ -532,7 +532,24 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
             x[ii][c] = lr + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(v)) : -__builtin_inff();
         }
     }
-    softmax_topk_rows<NB, 32, kF32, 32, RPW>(x, lr, lr, E, k, T, row, valid, wout, iout, eiout);
+    // all rows valid: one interleaved pass over the RPW rows; otherwise (the
+    // last, partly filled block: small batches) pairs of rows, skipping pairs
+    // past T (a top-k pass costs ~1 us per 4 rows with one wave per SIMD)
+    bool all = true;
+#pragma unroll
+    for (int ii = 0; ii < RPW; ++ii) all = all && valid[ii];
+    if (__all(all)) {
+        softmax_topk_rows<NB, 32, kF32, 32, RPW>(x, lr, lr, E, k, T, row, valid, wout, iout, eiout);
+    } else {
+#pragma unroll
+        for (int h = 0; h < RPW; h += 2) {
+            if (!__any(valid[h] || valid[h + 1])) continue;  // wave-uniform
+            const float(&xh)[2][NB] = reinterpret_cast<const float(&)[2][NB]>(x[h]);
+            const long long rh[2] = {row[h], row[h + 1]};
+            const bool vh[2] = {valid[h], valid[h + 1]};
+            softmax_topk_rows<NB, 32, kF32, 32, 2>(xh, lr, lr, E, k, T, rh, vh, wout, iout, eiout);
+        }
+    }
 }
 
 template <int DT, int NB>
