@@ -404,8 +404,10 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
 }
 
 // 16-bit router on the matrix cores (E > 32): one workgroup per 32*MT tokens
-// and NB waves, wave c computing the logits of experts 32c .. 32c+31 with
-// v_mfma_f32_32x32x16 (A = token rows, B = weight rows, both K-contiguous).
+// and NB*KH waves, wave (c, h) computing the logits of experts 32c .. 32c+31
+// with v_mfma_f32_32x32x16 (A = token rows, B = weight rows, both
+// K-contiguous) over the k16 steps h*4/KH .. (h+1)*4/KH-1 of every K tile;
+// the waves with h = 0 issue the DMA.
 // K tiles of 64 reach LDS by buffer_load ... lds in an NST-stage ring, each
 // instruction covering 8 rows x 128 contiguous bytes (row loads straight
 // into the MFMA fragment registers touch 32 rows per instruction, which the
@@ -413,10 +415,12 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
 // Rows of a stage hold 8 16-byte chunks, chunk c of row r at a_swz(r, c)
 // (conflict-free fragment reads). The result layout puts expert 32c + l%32
 // of token 32m + 8(i/4) + 4(l/32) + i%4 in register i of block m of lane l;
-// the waves swap blocks through LDS so that each holds whole tokens for the
-// softmax over 32-lane groups (VPT = NB experts per lane, stride 32).
-template <int DT, int NB, int MT, int NST>
-__global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __restrict__ xin,
+// the waves swap blocks through LDS (summing the KH partial products in
+// order) so that each holds whole tokens for the softmax over 32-lane groups
+// (VPT = NB experts per lane, stride 32); KH = 2 halves the rows each wave
+// ranks, whose top-k passes dominate small batches.
+template <int DT, int NB, int MT, int NST, int KH>
+__global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* __restrict__ xin,
                                                               const void* __restrict__ win,
                                                               float* __restrict__ wout, uint32_t* __restrict__ iout,
                                                               uint32_t* __restrict__ eiout, int T, int H, int E,
@@ -429,10 +433,12 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
     constexpr int INS = STAGE / 1024;             // DMA instructions per stage (8 rows each)
     constexpr int LOADS = INS / NB;               // per wave
     static_assert(LOADS * NB == INS && LOADS * (NST - 2) < 64, "router stage split");
-    static_assert(MT * NB * 16 * 64 * 4 <= NST * STAGE, "softmax exchange fits the ring");
+    static_assert(KH * MT * NB * 16 * 64 * 4 <= NST * STAGE, "softmax exchange fits the ring");
+    static_assert(KH == 1 || KH == 2, "K halves");
     __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cb = wave % NB, kh = wave / NB;  // expert block, K part
     const long long t0 = (long long)blockIdx.x * TM;  // < T (grid = ceil(T/TM))
     const int rows = T - t0 < TM ? (int)(T - t0) : TM;
     const i32x4 rx = make_rsrc(reinterpret_cast<const S*>(xin) + t0 * H, (long long)rows * H * 2);
@@ -447,7 +453,7 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
     bool is_x[LOADS];
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-        const int q = NB * i + wave;
+        const int q = NB * i + cb;
         const int row = 8 * q + lane / 8;  // row of the stage
         const int c = a_swz<8>(row, lane % 8);
         chunk_k[i] = 8 * c;
@@ -462,7 +468,7 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t v = (full || k0 + chunk_k[i] < H) ? off[i] : kOob;
-            dma16s(is_x[i] ? rx : rw, sl + (NB * i + wave) * 1024, v, (uint32_t)k0 * 2u);
+            dma16s(is_x[i] ? rx : rw, sl + (NB * i + cb) * 1024, v, (uint32_t)k0 * 2u);
         }
     };
 
@@ -472,9 +478,10 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
     const int lr = lane & 31, lh = lane >> 5;
+    const bool dma = kh == 0;
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
-        if (s < nk) issue(s, s * 64);
+        if (dma && s < nk) issue(s, s * 64);
     for (int kt = 0; kt < nk; ++kt) {
         // this wave's DMA of tile kt (NST-2 newer tiles may stay in flight),
         // then the barrier makes every wave's part visible and frees slot kt-1
@@ -486,13 +493,14 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
         else wait_vm<0>();
         wait_lgkm0();
         block_barrier();
-        if (kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt + NST - 1) * 64);
+        if (dma && kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt + NST - 1) * 64);
         const char* sx = smem + (kt % NST) * STAGE;
         const char* sw = sx + TM * 128;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+        for (int s4 = 0; s4 < 4 / KH; ++s4) {
+            const int st = kh * (4 / KH) + s4;
             const int c = 2 * st + lh;
-            const int wr = 32 * wave + lr;  // weight row; stage row TM + wr (the swizzle's row)
+            const int wr = 32 * cb + lr;  // weight row; stage row TM + wr (the swizzle's row)
             const u32x4 b = *reinterpret_cast<const u32x4*>(sw + wr * 128 + a_swz<8>(TM + wr, c) * 16);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
@@ -502,32 +510,35 @@ __global__ __launch_bounds__(64 * NB) void router_mfma_kernel(const void* __rest
             }
         }
     }
-    // exchange through LDS (the ring is free after the barrier): red[m][c][i][lane]
+    // exchange through LDS (the ring is free after the barrier):
+    // red[kh][m][c][i][lane]
     wait_lgkm0();
     __syncthreads();
     float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) red[((m * NB + wave) * 16 + i) * 64 + lane] = acc[m][i];
+        for (int i = 0; i < 16; ++i) red[(((kh * MT + m) * NB + cb) * 16 + i) * 64 + lane] = acc[m][i];
     __syncthreads();
-    // wave w takes result registers g = NB*ii + w ((m, i) = (g / 16, g % 16)):
+    // wave w takes result registers g = NW*ii + w ((m, i) = (g / 16, g % 16)):
     // the first tokens spread over all waves when the batch is small
-    constexpr int RPW = MT * 16 / NB;  // result registers per wave
-    static_assert(RPW * NB == MT * 16, "register split");
+    constexpr int NW = NB * KH;
+    constexpr int RPW = MT * 16 / NW;  // result registers per wave
+    static_assert(RPW * NW == MT * 16 && RPW % 2 == 0, "register split");
     float x[RPW][NB];
     long long row[RPW];
     bool valid[RPW];
 #pragma unroll
     for (int ii = 0; ii < RPW; ++ii) {
-        const int g = NB * ii + wave;
+        const int g = NW * ii + wave;
         const int m = g / 16, i = g % 16;
         const long long rw_ = t0 + 32 * m + 8 * (i / 4) + 4 * lh + (i % 4);
         valid[ii] = rw_ < T;
         row[ii] = valid[ii] ? rw_ : 0;
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
-            const float v = red[((m * NB + c) * 16 + i) * 64 + lane];
+            float v = red[((m * NB + c) * 16 + i) * 64 + lane];
+            if constexpr (KH == 2) v += red[(((MT + m) * NB + c) * 16 + i) * 64 + lane];
             // the logit as the matmul would store it in the input dtype
             x[ii][c] = lr + 32 * c < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(v)) : -__builtin_inff();
         }
@@ -562,11 +573,11 @@ static hipError_t launch_router_mfma(const void* x, const void* w, float* wo, ui
     if ((long long)T >= 256LL * 64) {
         const long long grid = ((long long)T + 63) / 64;
         if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 2, 3>), dim3((unsigned)grid), dim3(64 * NB), 0, stream, x, w,
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 2, 3, 2>), dim3((unsigned)grid), dim3(128 * NB), 0, stream, x, w,
                            wo, io, eo, T, H, E, k);
     } else {
         const long long grid = ((long long)T + 31) / 32;
-        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 1, 6>), dim3((unsigned)grid), dim3(64 * NB), 0, stream, x, w,
+        hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 1, 6, 2>), dim3((unsigned)grid), dim3(128 * NB), 0, stream, x, w,
                            wo, io, eo, T, H, E, k);
     }
     return hipGetLastError();
