@@ -596,9 +596,10 @@ static hipError_t launch_router_cfg(const void* x, const void* w, float* wo, uin
 template <int DT>
 static hipError_t launch_router_dt(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                    int H, int E, int k, hipStream_t stream) {
-    // 16-bit with more than 32 experts: the matrix-core kernel (2.5x faster
-    // than the FMA kernel at E=128); up to 32 experts the FMA kernel, whose
-    // coalesced row loads beat the MFMA kernel's strided fragments 2x
+    // 16-bit with more than 32 experts: the matrix-core kernel (several times
+    // faster than the FMA kernel at E=128); up to 32 experts the FMA kernel
+    // (at E=8 56 us against 72 us for the matrix-core kernel, whose weight
+    // block is then three quarters padding)
     if constexpr (DT != kF32) {
         if (E > 32 && E <= 64) return launch_router_mfma<DT, 2>(x, w, wo, io, eo, T, H, E, k, stream);
         if (E > 64) return launch_router_mfma<DT, 4>(x, w, wo, io, eo, T, H, E, k, stream);
