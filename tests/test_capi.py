@@ -197,3 +197,22 @@ def test_workspace_size():
     rc = L.candle_moe_fused_moe_ws(*([ctypes.c_void_p(256)] * 7), 32, 64, 256, 8, 2, 0, 0, 1,
                                    ctypes.c_void_p(256), 16, None)
     assert rc == cm.CANDLE_MOE_ERR_WORKSPACE
+
+
+def test_cpp_host_api_rejections(tmp_path):
+    """include/candle_moe.hpp compiles with the host C++ compiler alone and
+    its FusedMoE / apply_topk_softmax_inplace reject invalid calls with the
+    reference's messages (tests/cpp/host_api_rejections.cpp; no GPU)."""
+    import shutil
+    import subprocess
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        pytest.skip("no host C++ compiler")
+    libdir = os.path.join(ROOT, "candle-moe_amd")
+    exe = str(tmp_path / "host_api_rejections")
+    subprocess.run([cxx, "-std=c++17", "-O1", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "cpp", "host_api_rejections.cpp"), "-o", exe, "-L", libdir,
+                    "-lcandle_moe_hip", "-Wl,-rpath," + libdir], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
