@@ -251,7 +251,8 @@ __device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int
 //  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
 template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
-                                              int wm, int wn, int lane, const int32_t* s_tok, const float* s_w) {
+                                              int wm, int wn, int lane, const int32_t* s_tok, const float* s_w,
+                                              const int* pre_dst = nullptr, const float* pre_w = nullptr) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
     const int N = a.N;
@@ -281,9 +282,16 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
             if (ml >= m_valid) continue;
             const int r = r0 + ml;
             if constexpr (MODE == kGateUp || MODE == kFc1) {
-                const int p = a.sorted_pair[r];
-                const int dst = a.pair_dest ? a.pair_dest[p] : r;
-                const float wscale = a.fold_w ? a.routing_w[p] : 1.0f;
+                int dst;
+                float wscale;
+                if (pre_dst) {
+                    dst = pre_dst[mb];
+                    wscale = pre_w[mb];
+                } else {
+                    const int p = a.sorted_pair[r];
+                    dst = a.pair_dest ? a.pair_dest[p] : r;
+                    wscale = a.fold_w ? a.routing_w[p] : 1.0f;
+                }
                 uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)dst * N;
                 constexpr int PAIRS = DUAL ? NB / 2 : NB;
 #pragma unroll
@@ -310,7 +318,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                     }
                 }
             } else {
-                const int tok = a.tok_sorted[r];
+                const int tok = pre_dst ? pre_dst[mb] : a.tok_sorted[r];
                 uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)tok * N;
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {

@@ -365,6 +365,22 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             s_w[tid] = a.routing_w[p];
         }
     }
+    // gate/up, fc1: the epilogue's output rows and routing weights (two
+    // dependent reads per row), loaded now so that they are long done when the
+    // K loop ends. (The expert-set down GEMMs have no registers to spare for
+    // them and read their one row index in the epilogue.)
+    int pre_dst[MB];
+    float pre_w[MB];
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int ml = wm * WM + mb * 32 + (lane & 31);
+            const int r = r0 + (ml < m_valid ? ml : 0);
+            const int p = a.sorted_pair[r];
+            pre_dst[mb] = a.pair_dest ? a.pair_dest[p] : r;
+            pre_w[mb] = a.fold_w ? a.routing_w[p] : 1.0f;
+        }
+    }
 
     // Stage hand-over, one barrier per K tile: wait for this wave's DMA of
     // stage kt (the NST-2 newer stages may stay in flight) and for its own
@@ -489,7 +505,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         if (nsplit > 1 && !splitk_fixup<MB, NB, NW, FIX_BATCH>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
             return;
     }
-    tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w);
+    tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
+                                                GATHER ? pre_dst : nullptr, GATHER ? pre_w : nullptr);
 }
 
 template <int DT, int MODE>
