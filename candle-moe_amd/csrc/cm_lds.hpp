@@ -318,7 +318,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                     }
                 }
             } else {
-                const int tok = pre_dst ? pre_dst[mb] : a.tok_sorted[r];
+                // (moe_lds_gemm stages the tile's tokens in s_tok)
+                const int tok = pre_dst ? pre_dst[mb] : (s_tok ? s_tok[ml] : a.tok_sorted[r]);
                 uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)tok * N;
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     static_assert(BNK || SUB_INS * NSUB == B_INS, "B tile split");
     static_assert(LOADS * (NST - 2) < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
-    __shared__ int32_t s_tok[ATOMIC ? BM : 1];
+    __shared__ int32_t s_tok[(ATOMIC || SET) ? BM : 1];
     __shared__ float s_w[ATOMIC ? BM : 1];
 
     // workgroup -> (output tile, K split); every workgroup first clears its
@@ -365,10 +365,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             s_w[tid] = a.routing_w[p];
         }
     }
+    // expert-set down / fc2: the output row (token) of every tile row, staged
+    // in LDS now (no registers to spare) for the epilogue
+    if constexpr (SET) {
+        if (tid < BM) s_tok[tid] = a.tok_sorted[r0 + (tid < m_valid ? tid : 0)];
+    }
     // gate/up, fc1: the epilogue's output rows and routing weights (two
     // dependent reads per row), loaded now so that they are long done when the
-    // K loop ends. (The expert-set down GEMMs have no registers to spare for
-    // them and read their one row index in the epilogue.)
+    // K loop ends.
     int pre_dst[MB];
     float pre_w[MB];
     if constexpr (GATHER) {

@@ -337,7 +337,10 @@ __global__ __launch_bounds__(512, 1) void moe_pp_gemm(GemmArgs a) {
         }
     }
 
-    tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w);
+    // (s_tok holds the pair path's tokens only: the expert-set epilogue reads
+    // its rows from tok_sorted)
+    tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, ATOMIC ? s_tok : nullptr,
+                                                s_w);
 }
 
 template <int DT>
