@@ -422,3 +422,33 @@ def test_step_replayed_from_a_cuda_graph(T):
         assert torch.equal(out, ref)
         assert torch.equal(tw, ref_w) and torch.equal(ti, ref_i)
         assert torch.isfinite(eager.float()).all()
+
+
+@pytest.mark.parametrize("offset", [0, 1, 4])
+def test_pair_path_output_alignment(offset):
+    """The pair path's finalize reads and writes the caller's output 8
+    elements at a time when it is 16-byte aligned, one at a time otherwise
+    (an output that starts 2 or 8 bytes into an allocation): same result,
+    accumulated into the caller's values."""
+    import torch
+
+    T, H, I, E, k, dt = 48, 136, 64, 4, 2, O.BF16
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, 21, O.QWEN3)
+    init = O.round_to(O.randn((T, H), seed=22), dt)
+    buf = torch.zeros(T * H + 8, dtype=torch.bfloat16, device="cuda:0")
+    out = buf[offset:offset + T * H].view(T, H)
+    out.copy_(torch.from_numpy(init.astype(np.float32)).to("cuda:0").to(torch.bfloat16))
+    L = candle_moe.lib()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    tx, tg, tu, td = to_dev(x, dt), to_dev(G, dt), to_dev(U, dt), to_dev(D, dt)
+    trw, tri = to_dev(rw), to_dev(ri)
+    assert candle_moe.fused_moe_path(T, H, I, E, k, dt) == "pairs"
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    candle_moe.check(L.candle_moe_fused_moe_status(p(tx), p(tg), p(tu), p(td), p(trw), p(tri), p(out), T, H, I, E, k,
+                                                   O.SILU, O.QWEN3, dt, stream))
+    torch.cuda.synchronize()
+    want = O.fused_moe(x, G, U, D, rw, ri, E=E, k=k, act=O.SILU, moe_type=O.QWEN3, dtype=dt,
+                       mode=O.MODE_EXACT) + init.astype(np.float64)
+    assert_close(from_dev(out).astype(np.float64), want, RTOL[dt], f"output offset {offset}")
+    # the elements around the output are untouched
+    assert float(buf[:offset].abs().sum()) == 0.0 and float(buf[offset + T * H:].abs().sum()) == 0.0
