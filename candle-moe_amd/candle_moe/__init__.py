@@ -118,6 +118,10 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_profile_slot_name.restype = ctypes.c_char_p
         L.candle_moe_router_topk.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, u32, vp]
         L.candle_moe_router_topk.restype = i32
+        L.candle_moe_grouping_workspace_size.argtypes = [i32, i32]
+        L.candle_moe_grouping_workspace_size.restype = sz
+        L.candle_moe_group_pairs.argtypes = [vp, i32, i32, vp, vp, vp, sz, vp]
+        L.candle_moe_group_pairs.restype = i32
         L.candle_moe_trim_workspaces.argtypes = []
         L.candle_moe_trim_workspaces.restype = i32
         L.candle_moe_last_error.argtypes = []
@@ -220,6 +224,31 @@ def apply_topk_softmax_inplace(gating_output, topk_weight, topk_indices, token_e
     g, w, i, ei = (describe(t) for t in (gating_output, topk_weight, topk_indices, token_expert_indices))
     check(lib().candle_moe_apply_topk_softmax_inplace(
         ctypes.byref(g), ctypes.byref(w), ctypes.byref(i), ctypes.byref(ei), _stream_for(gating_output)))
+
+
+def group_pairs(expert_indices, num_experts: int):
+    """Token->expert grouping as fused_moe runs it (candle_moe_group_pairs):
+    expert_indices [T, k] (or flat) u32/i32 on the GPU -> (offsets [E+2] i32,
+    sorted_pairs [T*k] i32). offsets is the exclusive scan of the per-expert
+    counts with offsets[E] = valid pairs and offsets[E+1] = the largest count;
+    the first offsets[E] sorted_pairs are the pair ids t*k+j, grouped by expert,
+    ascending inside an expert; ids >= num_experts are dropped."""
+    import torch
+
+    idx = expert_indices.contiguous().view(-1)
+    P = idx.numel()
+    dev = idx.device
+    offsets = torch.empty(num_experts + 2, dtype=torch.int32, device=dev)
+    sorted_pairs = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+    n = lib().candle_moe_grouping_workspace_size(P, num_experts)
+    if n == 0:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "group_pairs: invalid sizes")
+    ws = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+    base = (ws.data_ptr() + 255) // 256 * 256
+    check(lib().candle_moe_group_pairs(ctypes.c_void_p(idx.data_ptr()), P, num_experts,
+                                       ctypes.c_void_p(offsets.data_ptr()), ctypes.c_void_p(sorted_pairs.data_ptr()),
+                                       ctypes.c_void_p(base), n, _stream_for(idx)))
+    return offsets, sorted_pairs[:P]
 
 
 def router_topk(hidden, router_weight, topk_weight, topk_indices, token_expert_indices) -> None:

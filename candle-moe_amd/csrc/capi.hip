@@ -173,6 +173,7 @@ static long long set_tiles_max(const Problem& p) {
 }
 
 static size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t a256_bytes(size_t x) { return a256(x); }
 
 static Layout make_layout(const Problem& p) {
     Layout L;
@@ -672,6 +673,52 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
     return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
                               num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
                               activation_type, moe_type, dtype, workspace, workspace_bytes, false, false, stream);
+}
+
+// Scratch of candle_moe_group_pairs: per-block counts and the row-tile table
+// (256-row tiles) of the grouping.
+static size_t group_pairs_ws(long long P, int E) {
+    const long long nb = cm::grouping_blocks(P);
+    const long long mt = cm::grouping_max_tiles(P, E, 256);
+    return cm::a256_bytes((size_t)(nb > 0 ? nb : 1) * E * 4) + 2 * cm::a256_bytes((size_t)(mt > 0 ? mt : 1) * 4) + 256;
+}
+
+size_t candle_moe_grouping_workspace_size(int num_pairs, int num_experts) {
+    if (num_pairs < 0 || num_experts < 1 || num_experts > 4096) return 0;
+    return group_pairs_ws(num_pairs, num_experts);
+}
+
+int candle_moe_group_pairs(const void* expert_indices, int num_pairs, int num_experts, void* offsets,
+                           void* sorted_pairs, void* workspace, size_t workspace_bytes, void* stream) {
+    cm::clear_error();
+    const int P = num_pairs, E = num_experts;
+    if (P < 0) return cm::set_error(CANDLE_MOE_ERR_INVALID, "group_pairs: num_pairs must be >= 0 (got %d)", P);
+    if (E < 1 || E > 4096)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "group_pairs: num_experts must be in [1, 4096] (got %d)", E);
+    if (!offsets || (P > 0 && (!expert_indices || !sorted_pairs)))
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "group_pairs: null pointer");
+    const size_t need = group_pairs_ws(P, E);
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256))
+        return cm::set_error(CANDLE_MOE_ERR_WORKSPACE,
+                             "group_pairs: workspace must be 256-byte aligned and hold %zu bytes (got %zu)", need,
+                             workspace_bytes);
+    char* ws = reinterpret_cast<char*>(workspace);
+    const long long nb = cm::grouping_blocks(P);
+    const long long mt = cm::grouping_max_tiles(P, E, 256);
+    cm::GroupingBufs gb = {};
+    gb.offsets = reinterpret_cast<int32_t*>(offsets);
+    gb.sorted_pair = reinterpret_cast<int32_t*>(sorted_pairs);
+    gb.block_counts = reinterpret_cast<int32_t*>(ws);
+    ws += cm::a256_bytes((size_t)(nb > 0 ? nb : 1) * E * 4);
+    gb.tile_row = reinterpret_cast<int32_t*>(ws);
+    ws += cm::a256_bytes((size_t)(mt > 0 ? mt : 1) * 4);
+    gb.tile_exp = reinterpret_cast<int32_t*>(ws);
+    ws += cm::a256_bytes((size_t)(mt > 0 ? mt : 1) * 4);
+    gb.num_tiles = reinterpret_cast<int32_t*>(ws);
+    const cm::GroupJob pj =
+        cm::pair_grouping_job(reinterpret_cast<const uint32_t*>(expert_indices), P, E, 256, gb);
+    const hipError_t e = cm::launch_groupings(pj, nullptr, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "group_pairs launch");
 }
 
 int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight, void* topk_indices,

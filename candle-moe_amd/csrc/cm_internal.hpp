@@ -54,6 +54,7 @@ struct GroupJob {
 GroupJob pair_grouping_job(const uint32_t* idx, long long P, int E, int BM, const GroupingBufs& b);
 GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
                           int32_t* pair_dest);
+size_t a256_bytes(size_t x);  // x rounded up to 256 bytes
 // The pair grouping and optionally the token grouping, in at most three launches.
 hipError_t launch_groupings(const GroupJob& pairs, const GroupJob* tokens, hipStream_t stream);
 

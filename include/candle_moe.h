@@ -164,6 +164,23 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
                            void* topk_indices, void* token_expert_indices, int num_tokens,
                            int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);
 
+/* Token->expert grouping as fused_moe runs it internally (the reference's
+ * launch_preprocessing, /root/reference/kernels/preprocessing.cuh:5-313, which
+ * has no exported symbol; exposed for callers that route themselves and for
+ * tests). Pairs p of expert_indices [num_pairs] u32 (p = t*k + j) are grouped
+ * by expert, stable (ascending p inside an expert); ids >= num_experts are
+ * dropped.
+ *   offsets [num_experts + 2] i32: exclusive scan of the per-expert counts,
+ *     offsets[E] = valid pairs, offsets[E+1] = largest count;
+ *   sorted_pairs [num_pairs] i32: the first offsets[E] entries are the valid
+ *     pair ids in that order (the reference stores the token ids p / k and the
+ *     weights w[p] instead; both follow from the pair id).
+ * workspace: candle_moe_grouping_workspace_size(num_pairs, num_experts) bytes,
+ * 256-byte aligned; nothing is allocated. Asynchronous on `stream`. */
+size_t candle_moe_grouping_workspace_size(int num_pairs, int num_experts);
+int candle_moe_group_pairs(const void* expert_indices, int num_pairs, int num_experts, void* offsets,
+                           void* sorted_pairs, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status
  * and the FusedMoE forward (hipFreeAsync on the stream each was used on); the
  * next call allocates again. No counterpart in the reference, whose fused_moe

@@ -216,3 +216,14 @@ def test_cpp_host_api_rejections(tmp_path):
                     "-lcandle_moe_hip", "-Wl,-rpath," + libdir], check=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
+
+
+def test_grouping_entry_point_rejects_without_launch():
+    L = cm.lib()
+    assert L.candle_moe_grouping_workspace_size(0, 0) == 0
+    assert L.candle_moe_grouping_workspace_size(100, 8) > 0
+    assert L.candle_moe_group_pairs(None, -1, 8, None, None, None, 0, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert "num_pairs" in cm.last_error()
+    assert L.candle_moe_group_pairs(None, 4, 5000, None, None, None, 0, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_group_pairs(ctypes.c_void_p(256), 4, 8, ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                    ctypes.c_void_p(256), 16, None) == cm.CANDLE_MOE_ERR_WORKSPACE
