@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace cm {
 
 // dtype codes of the C ABI (/root/reference/src/lib.rs:174-182)
@@ -38,6 +40,19 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
     _Float16 h = (_Float16)f;
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+// Two f32 values rounded to nearest even and packed, a in the low half: one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 for the pair.
+template <int DT> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {a, b};
+    if constexpr (DT == kBF16) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    } else {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    }
 }
 
 template <int DT> struct Elem;
@@ -75,17 +90,38 @@ __device__ __forceinline__ float act_f32(float x, int act) {
 //   silu(x) = x * 1 / (1 + 2^(-x log2 e))
 //   gelu(x) = x * 1 / (1 + 2^(-2 log2 e * sqrt(2/pi) (x + 0.044715 x^3)))
 //             (0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)))
-__device__ __forceinline__ float act_fast(float x, int act) {
-    if (act == kRelu) return fmaxf(x, 0.0f);
-    float z;
-    if (act == kGelu) {
-        const float k = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
-        z = k * (x + 0.044715f * x * x * x);
+// For x -> -inf, 2^z overflows to +inf and v_rcp_f32(+inf) = 0, so the
+// result goes to (-)0 as x / (1 + e^-x) does; x = -inf gives NaN in both.
+template <int ACT> __device__ __forceinline__ float act_t(float x) {
+    if constexpr (ACT == kRelu) {
+        return fmaxf(x, 0.0f);
     } else {
-        z = -1.4426950408889634f * x;
+        float z;
+        if constexpr (ACT == kGelu) {
+            const float k = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+            z = k * (x + 0.044715f * x * x * x);
+        } else {
+            z = -1.4426950408889634f * x;
+        }
+        return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
     }
-    // clamp keeps 2^z finite (the quotient is then 0 to f32 precision)
-    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fminf(z, 126.0f)));
+}
+__device__ __forceinline__ float act_fast(float x, int act) {
+    if (act == kRelu) return act_t<kRelu>(x);
+    if (act == kGelu) return act_t<kGelu>(x);
+    return act_t<kSilu>(x);
+}
+// f(std::integral_constant<int, ACT>{}) for the runtime activation code, so
+// that a loop over elements inside f is compiled once per activation with no
+// per-element branch.
+template <class F> __device__ __forceinline__ void with_act(int act, F&& f) {
+    if (act == kGelu) {
+        f(std::integral_constant<int, kGelu>{});
+    } else if (act == kRelu) {
+        f(std::integral_constant<int, kRelu>{});
+    } else {
+        f(std::integral_constant<int, kSilu>{});
+    }
 }
 
 // ---------------------------------------------------------------------

@@ -294,29 +294,33 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                 }
                 uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)dst * N;
                 constexpr int PAIRS = DUAL ? NB / 2 : NB;
+                with_act(a.act, [&](auto act_c) {
+                    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-                for (int q = 0; q < PAIRS; ++q) {
-                    const int colbase = DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
+                    for (int q = 0; q < PAIRS; ++q) {
+                        const int colbase =
+                            DUAL ? nt * (BN / 2) + ((wn * WN) / 64 + q) * 32 : nt * BN + wn * WN + q * 32;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int col = colbase + 8 * g + nsub;
-                        if (col >= N) continue;
-                        float h[4];
+                        for (int g = 0; g < 4; ++g) {
+                            const int col = colbase + 8 * g + nsub;
+                            if (col >= N) continue;
+                            float h[4];
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            if constexpr (DUAL) {
-                                h[j] = act_fast(acc[mb][2 * q][4 * g + j], a.act) * acc[mb][2 * q + 1][4 * g + j];
-                            } else {
-                                h[j] = act_fast(acc[mb][q][4 * g + j], a.act);
+                            for (int j = 0; j < 4; ++j) {
+                                if constexpr (DUAL) {
+                                    h[j] = act_t<ACT>(acc[mb][2 * q][4 * g + j]) * acc[mb][2 * q + 1][4 * g + j];
+                                } else {
+                                    h[j] = act_t<ACT>(acc[mb][q][4 * g + j]);
+                                }
+                                h[j] *= wscale;
                             }
-                            h[j] *= wscale;
+                            u32x2 v;
+                            v[0] = pack2<DT>(h[0], h[1]);
+                            v[1] = pack2<DT>(h[2], h[3]);
+                            *reinterpret_cast<u32x2*>(C + col) = v;
                         }
-                        u32x2 v;
-                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
-                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
-                        *reinterpret_cast<u32x2*>(C + col) = v;
                     }
-                }
+                });
             } else {
                 // (moe_lds_gemm stages the tile's tokens in s_tok)
                 const int tok = pre_dst ? pre_dst[mb] : (s_tok ? s_tok[ml] : a.tok_sorted[r]);
@@ -337,8 +341,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                         h[2] = Elem<DT>::to_f32((uint16_t)(old[1] & 0xffffu)) + acc[mb][nb][4 * g + 2];
                         h[3] = Elem<DT>::to_f32((uint16_t)(old[1] >> 16)) + acc[mb][nb][4 * g + 3];
                         u32x2 v;
-                        v[0] = (uint32_t)Elem<DT>::from_f32(h[0]) | ((uint32_t)Elem<DT>::from_f32(h[1]) << 16);
-                        v[1] = (uint32_t)Elem<DT>::from_f32(h[2]) | ((uint32_t)Elem<DT>::from_f32(h[3]) << 16);
+                        v[0] = pack2<DT>(h[0], h[1]);
+                        v[1] = pack2<DT>(h[2], h[3]);
                         *reinterpret_cast<u32x2*>(C + col) = v;
                     }
                 }
