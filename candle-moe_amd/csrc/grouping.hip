@@ -80,14 +80,21 @@ __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
     const int wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
     __syncthreads();
+    constexpr int IPT = kGroupChunk / kGroupThreads;  // items per thread
     const long long base = (long long)blk * kGroupChunk;
-    const long long end = base + kGroupChunk < P ? base + kGroupChunk : P;
     int32_t* mine = s_cnt + wave * nbins;
     int rank[kSetMaxK];
-    for (long long p = base + threadIdx.x; p < end; p += kGroupThreads) {
-        const int b = item_bin<TOK>(idx, p, k, E, rank);
-        if (b >= 0) atomicAdd(mine + b, 1);
+    // the bins of all IPT items first, so that their loads are in flight
+    // together, then the LDS counts
+    int bin[IPT];
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        const long long p = base + s * kGroupThreads + threadIdx.x;
+        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
     }
+#pragma unroll
+    for (int s = 0; s < IPT; ++s)
+        if (bin[s] >= 0) atomicAdd(mine + bin[s], 1);
     __syncthreads();
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads)
         block_counts[(long long)blk * nbins + e] =
@@ -179,9 +186,13 @@ __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
         for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) s_bc[i] = block_counts[i];
         __syncthreads();
     }
-    if (staged) {
-        // one thread per bin walks its column of the staged counts (the LDS
-        // reads are independent, only the running sum is serial)
+    // Few bins over many blocks (the pair grouping): each wave scans whole
+    // bins, its lanes over the blocks 64 at a time. Otherwise (the token-set
+    // grouping: many bins, fewer blocks) one thread per bin walks its column
+    // of the staged counts (the LDS reads are independent, only the running
+    // sum is serial).
+    const bool by_wave = !staged || ((nbins + kGroupThreads / 64 - 1) / (kGroupThreads / 64)) * 2 < nblocks;
+    if (staged && !by_wave) {
         for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
             int32_t run = 0;
             for (int b = 0; b < nblocks; ++b) {
@@ -193,8 +204,8 @@ __device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
             s_tb[e] = (run + BM - 1) / BM;
         }
     }
-    int32_t* bc = block_counts;
-    for (int e = wave; e < (staged ? 0 : nbins); e += kGroupThreads / 64) {
+    int32_t* bc = staged ? s_bc : block_counts;
+    for (int e = wave; e < (by_wave ? nbins : 0); e += kGroupThreads / 64) {
         int32_t carry = 0;
         for (int b0 = 0; b0 < nblocks; b0 += 64) {
             const int b = b0 + lane;
