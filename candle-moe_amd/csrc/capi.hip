@@ -248,9 +248,13 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     //  * at most 128, where the 256x256 tile would leave fewer than 256
     //    workgroups (few experts): the 128x128 tile, which doubles to
     //    quadruples the workgroups;
-    //  * at most 1024 with a hidden size of at most 2048 (short K loops of
+    //  * fewer than 1024 with a hidden size of at most 2048 (short K loops of
     //    the gate/up GEMM): the 128x256 tile, two workgroups per CU, so that
-    //    one's prologue, barriers and epilogue overlap the other's MFMAs;
+    //    one's prologue, barriers and epilogue overlap the other's MFMAs --
+    //    if the down GEMM's 128x256 tiles fill both slots of every CU; with
+    //    a small hidden size (Nomic, H = 768: 3 column tiles) they do not,
+    //    and the 256x256 tile, whose partly filled last round is split along
+    //    K, is faster (Nomic T=2048 / 4096 steps 192 / 219 -> 119 / 198 us);
     //  * otherwise the 256x256 tile with 8 waves.
     // Expected live row tiles of a tile height: one per touched expert at
     // least, the rows over the tile height at least.
@@ -270,7 +274,8 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
-        else if (H <= 2048 && P <= 1024 * touched) p.cfg = kLds128x256o2;
+        else if (H <= 2048 && P < 1024 * touched && (long long)cdiv(H, 256) * est_tiles(128) >= 512)
+            p.cfg = kLds128x256o2;
     }
     // the LDS-DMA kernels address operands with 32-bit buffer offsets
     if (is_lds_cfg(p.cfg)) {
