@@ -285,8 +285,12 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     }
     p.BM = tile_rows(p.cfg);
     // Expert-set path: each distinct sorted expert set becomes one GEMM group
-    // over K = k*I; worth it when the sets are few next to the tokens (on
-    // average at least half a row tile per set, e.g. E=8, k=2 from T >= 1792).
+    // over K = k*I; worth it when the sets are few next to the tokens: on
+    // average at least half a row tile per set where the hidden size is large
+    // (the pair path's f32 combine and finalize grow with H; Qwen3, H = 4096,
+    // BM = 256: sets from T >= 3584), 1.4 row tiles with a small hidden size
+    // (Nomic, H = 768: pairs 267 against 312 us at T=8192, sets 379 against
+    // 404 us at T=12288).
     p.set_path = false;
     p.nkeys = 0;
     if (p.mfma && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
@@ -297,7 +301,8 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             for (int j = 0; j < k; ++j) sets = sets * (E - j) / (j + 1);
             if (sets < 1.0) sets = 1.0;
             p.nkeys = (int)nk;
-            p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= 0.5 * p.BM * sets);
+            const double fill = H >= 2048 ? 0.5 : 1.4;
+            p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets);
         }
     }
     // K splits for the 32-row (decode) GEMMs and the f32 kernels, whose output
