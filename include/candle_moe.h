@@ -138,7 +138,8 @@ int candle_moe_set_combine_policy(int policy);
  * 12 = 32x256 (default when experts get <= 32 rows on average),
  * 13 / 14 = 256x128 / 128x256 (BK 32, two workgroups per CU). By default 5
  * is taken for <= 128 rows per expert where the 256x256 tile would give few
- * workgroups, 14 for <= 1024 rows per expert with hidden_dim <= 2048, else 7.
+ * workgroups, 14 for < 1024 rows per expert with hidden_dim <= 2048 when the
+ * down GEMM has at least two 128x256 tiles per CU, else 7.
  * f32 (vector FMA): 15 = 32x128 tile, 16 = 128x128 tile, both with K splits
  * when the tiles are few; by default 15 for <= 32 rows per expert, else 16
  * (the scalar 64x64 kernel 0 when hidden_dim or intermediate_dim is not a
@@ -146,7 +147,7 @@ int candle_moe_set_combine_policy(int policy);
 int candle_moe_set_tile_policy(int policy);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
- * bits 2-5: the GEMM kernel (policy code above); -1 = invalid sizes. */
+ * bits 2 and up: the GEMM kernel (policy code above); -1 = invalid sizes. */
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype);
 
