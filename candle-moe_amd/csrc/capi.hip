@@ -134,6 +134,7 @@ struct Problem {
     int n_tiles1, n_tiles2;
     bool lds_family;  // both GEMMs run moe_lds_gemm (fused clears and K splits available)
     bool fused_clear_ok;  // the gate/up kernel can clear the pair path's accumulator
+    bool rows_path;   // pair path: each pair's weighted down row stored, then summed per token (no atomics)
     int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
     int split_target; // K splits: the kernels aim at this many workgroups (live tiles * splits)
 };
@@ -201,8 +202,8 @@ static Layout make_layout(const Problem& p) {
         L.k_offsets = L.k_block_counts = L.tok_sorted = L.tile_row2 = L.tile_key2 = L.num_tiles2 = L.pair_dest = 0;
     }
     L.inter = o; o += a256((size_t)p.P * p.I * es);
-    L.acc = o;
-    if (!p.set_path) o += a256((size_t)p.T * p.H * 4);
+    L.acc = o;  // pair path: f32 accumulator [T, H], or the pair rows [T*k, H] (dtype)
+    if (!p.set_path) o += p.rows_path ? a256((size_t)p.P * p.H * es) : a256((size_t)p.T * p.H * 4);
     // split-K partials and arrival counters, shared by the two GEMMs (they run
     // one after the other; the counters are left zero)
     L.partial = L.counters = o;
@@ -320,6 +321,14 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     //    136 us against 150-190 us with the device's one-round choice).
     p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
     p.fused_clear_ok = p.lds_family || is_f32_cfg(p.cfg);
+    // Pair path on the LDS-DMA kernels (16-bit): the down GEMM stores each
+    // pair's weighted row once and a row-contiguous pass sums a token's k
+    // rows, instead of f32 atomics into [T, H] and a finalize pass (the
+    // atomics were 27-42 % of the down GEMM on Qwen3 T=2048 and the
+    // Qwen3-30B-A3B shapes). Deterministic for every k. Not for the 32-row
+    // decode kernels, whose few atomics cost less than the k-row pass
+    // (Qwen3-30B-A3B T=16: 90 against 94 us).
+    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
     p.split1 = p.split2 = 1;
@@ -426,7 +435,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.counters = counters;
     g1.tail_cus = p.tail_cus;
     // the gate/up workgroups clear the pair path's accumulator
-    const bool fused_clear = !p.set_path && p.fused_clear_ok;
+    const bool fused_clear = !p.set_path && !p.rows_path && p.fused_clear_ok;
     if (fused_clear) {
         g1.zero_f32 = acc;
         g1.zero_n = (long long)p.T * p.H;
@@ -476,7 +485,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         return CANDLE_MOE_OK;
     }
 
-    if (!fused_clear) {
+    if (!fused_clear && !p.rows_path) {
         ProfScope ps(kSlotZero, s);
         e = launch_fill_zero_f32(acc, (long long)p.T * p.H, s);
         if (e != hipSuccess) return hip_fail(e, "fused_moe accumulator clear");
@@ -486,13 +495,13 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.A = inter;
     g2.B0 = qwen3 ? down : up;
     g2.B1 = nullptr;
-    g2.C = acc;
+    g2.C = p.rows_path ? static_cast<void*>(ws + L.acc) : static_cast<void*>(acc);
     g2.strideB = (long long)p.I * p.H;
     g2.ldb = qwen3 ? p.H : p.I;
     g2.K = p.I;
     g2.N = p.H;
     g2.a_bytes = p.P * p.I * (p.dtype == kF32 ? 4 : 2);
-    const int mode2 = qwen3 ? kDown : kFc2;
+    const int mode2 = p.rows_path ? (qwen3 ? kDownRows : kFc2Rows) : (qwen3 ? kDown : kFc2);
     g2.n_tiles = p.n_tiles2;
     g2.ksplit = p.split2;
     g2.split_target = p.split_target;
@@ -508,7 +517,9 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
 
     {
         ProfScope ps(kSlotFinal, s);
-        e = launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, overwrite, s);
+        e = p.rows_path ? launch_pair_rows_sum(out, p.dtype, ws + L.acc, static_cast<const uint32_t*>(idx), p.E,
+                                               p.T, p.k, p.H, overwrite, s)
+                        : launch_finalize(out, p.dtype, acc, (long long)p.T * p.H, overwrite, s);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe finalize");
     return CANDLE_MOE_OK;

@@ -66,6 +66,8 @@ enum GemmMode : int {
     kFc2 = 3,      // Nomic: acc[t] += w * (inter.U^T)     (A = inter rows, B [N,K], f32 atomics)
     kDownSet = 4,  // Qwen3, tokens grouped by expert set: out[t] += [w*h_1 .. w*h_k] . [D_e1; ..; D_ek]
     kFc2Set = 5,   // Nomic, same with the U_e^T blocks
+    kDownRows = 6, // Qwen3, pair path without atomics: rows[p] = dtype(w_p * (inter.D))  (rows [T*k, N])
+    kFc2Rows = 7,  // Nomic, same with U^T
 };
 
 struct GemmArgs {
@@ -173,6 +175,11 @@ hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);
 hipError_t launch_fill_zero_bytes(void* p, long long nbytes, hipStream_t stream);
+// out[t] = dtype(out[t] + sum_j rows[t*k + j]), or without out[t] with
+// overwrite (rows: [T*k, H] of the output dtype, f32 sums in slot order;
+// slots whose expert idx[t*k + j] >= E were dropped and have no row)
+hipError_t launch_pair_rows_sum(void* out, int dtype, const void* rows, const uint32_t* idx, int E, int T, int k,
+                                int H, bool overwrite, hipStream_t stream);
 // out[i] = dtype(out[i] + acc[i]), or dtype(acc[i]) with overwrite
 hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, bool overwrite, hipStream_t stream);
 

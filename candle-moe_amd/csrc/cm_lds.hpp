@@ -249,6 +249,7 @@ __device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int
 //  kDownSet/kFc2Set: out[tok] = dtype(out[tok] + acc), or dtype(acc) with overwrite
 //                   (each output row is owned by one tile)
 //  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
+//  kDownRows / kFc2Rows: rows[p] = dtype(w * acc)      (the pair's own row)
 template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
                                               int wm, int wn, int lane, const int32_t* s_tok, const float* s_w,
@@ -321,6 +322,24 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                         }
                     }
                 });
+            } else if constexpr (MODE == kDownRows || MODE == kFc2Rows) {
+                // the pair's own row: rows[p] = dtype(w_p * acc)
+                const int p = pre_dst ? pre_dst[mb] : a.sorted_pair[r];
+                const float wscale = pre_w ? pre_w[mb] : a.routing_w[p];
+                uint16_t* C = reinterpret_cast<uint16_t*>(a.C) + (long long)p * N;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int colbase = nt * BN + wn * WN + nb * 32;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = colbase + 8 * g + nsub;
+                        if (col >= N) continue;
+                        u32x2 v;
+                        v[0] = pack2<DT>(wscale * acc[mb][nb][4 * g + 0], wscale * acc[mb][nb][4 * g + 1]);
+                        v[1] = pack2<DT>(wscale * acc[mb][nb][4 * g + 2], wscale * acc[mb][nb][4 * g + 3]);
+                        *reinterpret_cast<u32x2*>(C + col) = v;
+                    }
+                }
             } else {
                 // (moe_lds_gemm stages the tile's tokens in s_tok)
                 const int tok = pre_dst ? pre_dst[mb] : (s_tok ? s_tok[ml] : a.tok_sorted[r]);

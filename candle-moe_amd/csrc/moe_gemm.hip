@@ -528,6 +528,79 @@ hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream) {
     return launch_fill_zero_bytes(p, n * 4, stream);
 }
 
+// Pair rows -> token rows: one thread per 8 consecutive columns of a token
+// (16-byte loads of its k rows, f32 sums in slot order, one 16-byte store).
+template <int DT>
+__global__ void pair_rows_sum8_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ rows,
+                                      const uint32_t* __restrict__ idx, int E, int T, int k, int H, int overwrite) {
+    const int h8 = H / 8;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < (long long)T * h8;
+         i += (long long)gridDim.x * blockDim.x) {
+    const long long t = i / h8, c = (i - t * h8) * 8;
+    float s[8];
+    if (overwrite) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+    } else {
+        const u32x4 o = *reinterpret_cast<const u32x4*>(out + t * H + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[2 * j] = Elem<DT>::to_f32((uint16_t)(o[j] & 0xffffu));
+            s[2 * j + 1] = Elem<DT>::to_f32((uint16_t)(o[j] >> 16));
+        }
+    }
+    for (int j = 0; j < k; ++j) {
+        if (idx[t * k + j] >= (uint32_t)E) continue;  // dropped pair: no row
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows + (t * k + j) * H + c));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            s[2 * q] += Elem<DT>::to_f32((uint16_t)(v[q] & 0xffffu));
+            s[2 * q + 1] += Elem<DT>::to_f32((uint16_t)(v[q] >> 16));
+        }
+    }
+    u32x4 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = pack2<DT>(s[2 * q], s[2 * q + 1]);
+    *reinterpret_cast<u32x4*>(out + t * H + c) = r;
+    }
+}
+template <int DT>
+__global__ void pair_rows_sum_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ rows,
+                                     const uint32_t* __restrict__ idx, int E, int T, int k, int H, int overwrite) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < (long long)T * H;
+         i += (long long)gridDim.x * blockDim.x) {
+        const long long t = i / H, c = i - t * H;
+        float s = overwrite ? 0.0f : Elem<DT>::to_f32(out[i]);
+        for (int j = 0; j < k; ++j)
+            if (idx[t * k + j] < (uint32_t)E) s += Elem<DT>::to_f32(rows[(t * k + j) * H + c]);
+        out[i] = Elem<DT>::from_f32(s);
+    }
+}
+
+hipError_t launch_pair_rows_sum(void* out, int dtype, const void* rows, const uint32_t* idx, int E, int T, int k,
+                                int H, bool overwrite, hipStream_t stream) {
+    if (T <= 0 || H <= 0) return hipSuccess;
+    if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
+    const int ow = overwrite ? 1 : 0;
+    uint16_t* o = reinterpret_cast<uint16_t*>(out);
+    const uint16_t* rw = reinterpret_cast<const uint16_t*>(rows);
+    const dim3 b(256);
+    if (H % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)rows % 16) == 0) {
+        const dim3 g(grid_for((long long)T * (H / 8), 256));
+        if (dtype == kBF16)
+            hipLaunchKernelGGL(pair_rows_sum8_kernel<kBF16>, g, b, 0, stream, o, rw, idx, E, T, k, H, ow);
+        else
+            hipLaunchKernelGGL(pair_rows_sum8_kernel<kF16>, g, b, 0, stream, o, rw, idx, E, T, k, H, ow);
+    } else {
+        const dim3 g(grid_for((long long)T * H, 256));
+        if (dtype == kBF16)
+            hipLaunchKernelGGL(pair_rows_sum_kernel<kBF16>, g, b, 0, stream, o, rw, idx, E, T, k, H, ow);
+        else
+            hipLaunchKernelGGL(pair_rows_sum_kernel<kF16>, g, b, 0, stream, o, rw, idx, E, T, k, H, ow);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_finalize(void* out, int dtype, const float* acc, long long n, bool overwrite, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const dim3 g(grid_for(n, 256)), b(256);

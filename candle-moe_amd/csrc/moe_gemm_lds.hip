@@ -43,7 +43,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
     constexpr bool SET = (MODE == kDownSet || MODE == kFc2Set);
-    constexpr bool BNK = (MODE == kFc2 || MODE == kFc2Set);
+    constexpr bool BNK = (MODE == kFc2 || MODE == kFc2Set || MODE == kFc2Rows);
+    constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
     constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
     constexpr bool SWAP = !ATOMIC;
     static_assert(BK == 32 || BK == 64, "BK");
@@ -373,16 +374,22 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // gate/up, fc1: the epilogue's output rows and routing weights (two
     // dependent reads per row), loaded now so that they are long done when the
     // K loop ends.
+    // (pair-row down / fc2: the row's pair and its routing weight)
     int pre_dst[MB];
     float pre_w[MB];
-    if constexpr (GATHER) {
+    if constexpr (GATHER || ROWS) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
             const int ml = wm * WM + mb * 32 + (lane & 31);
             const int r = r0 + (ml < m_valid ? ml : 0);
             const int p = a.sorted_pair[r];
-            pre_dst[mb] = a.pair_dest ? a.pair_dest[p] : r;
-            pre_w[mb] = a.fold_w ? a.routing_w[p] : 1.0f;
+            if constexpr (ROWS) {
+                pre_dst[mb] = p;
+                pre_w[mb] = a.routing_w[p];
+            } else {
+                pre_dst[mb] = a.pair_dest ? a.pair_dest[p] : r;
+                pre_w[mb] = a.fold_w ? a.routing_w[p] : 1.0f;
+            }
         }
     }
 
@@ -510,7 +517,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             return;
     }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
-                                                GATHER ? pre_dst : nullptr, GATHER ? pre_w : nullptr);
+                                                (GATHER || ROWS) ? pre_dst : nullptr,
+                                                (GATHER || ROWS) ? pre_w : nullptr);
 }
 
 template <int DT, int MODE>
@@ -580,12 +588,17 @@ static hipError_t launch_lds_dt(int mode, int cfg, const GemmArgs& a, hipStream_
         case kFc2: return launch_lds_mode<DT, kFc2>(cfg, a, stream);
         case kDownSet: return launch_lds_mode<DT, kDownSet>(cfg, a, stream);
         case kFc2Set: return launch_lds_mode<DT, kFc2Set>(cfg, a, stream);
+        case kDownRows: return launch_lds_mode<DT, kDownRows>(cfg, a, stream);
+        case kFc2Rows: return launch_lds_mode<DT, kFc2Rows>(cfg, a, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
-    if (cfg == kPingPong) return launch_moe_gemm_pp(mode, dtype, a, stream);
+    if (cfg == kPingPong) {
+        if (mode == kDownRows || mode == kFc2Rows) return hipErrorInvalidValue;
+        return launch_moe_gemm_pp(mode, dtype, a, stream);
+    }
     if (dtype == kBF16) return launch_lds_dt<kBF16>(mode, cfg, a, stream);
     if (dtype == kF16) return launch_lds_dt<kF16>(mode, cfg, a, stream);
     return hipErrorInvalidValue;
