@@ -125,7 +125,9 @@ int candle_moe_profile_end(double* total_ms, int* counts, int nslots);
 const char* candle_moe_profile_slot_name(int slot);
 
 /* Combine strategy of fused_moe (process-wide): 0 = choose per call (default),
- * 1 = always the pair path (f32 accumulator + atomic scatter-add),
+ * 1 = always the pair path (the down GEMM over expert-sorted pairs; each
+ *     pair's weighted row stored and a token's k rows summed, or, on the
+ *     32-row decode and f32 kernels, f32 atomics into an accumulator),
  * 2 = the expert-set path whenever the shape allows it (MFMA dtypes,
  *     intermediate_dim % 64 == 0, (E+1)^k <= 1024, k <= 8). */
 int candle_moe_set_combine_policy(int policy);
