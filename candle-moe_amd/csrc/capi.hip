@@ -165,6 +165,9 @@ struct Layout {
 
 // 0: choose per call; 1: always the pair path (f32 atomics); 2: the
 // expert-set path whenever the shape allows it.
+// Pair-row bytes (T*k*H 16-bit values) from which the expert-set path is
+// preferred over the pair path's row stores and k-row sums.
+constexpr double kSetMinRowBytes = 256.0 * 1024 * 1024;
 static int g_combine_policy = 0;
 // 0: choose the MFMA tile per call; kTile128 / kTile256: force it.
 static int g_tile_policy = 0;
@@ -303,7 +306,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             if (sets < 1.0) sets = 1.0;
             p.nkeys = (int)nk;
             const double fill = H >= 2048 ? 0.5 : 1.4;
-            p.set_path = g_combine_policy == 2 || (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets);
+            // Against the pair path's row stores and k-row sums (16-bit
+            // LDS-DMA kernels) the expert sets pay off only once those rows
+            // are large: Qwen3 T=4096 / 8192 pairs 454 / 792 against sets 484 /
+            // 830 us, T=32768 (537 MB of rows) sets 2346 against 2499 us;
+            // Nomic T=12288 / 32768 pairs 377 / 859 against 390 / 899 us.
+            const bool rows_ok = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong && p.dtype != kF32;
+            const bool big_rows = (double)P * H * 2.0 >= (double)kSetMinRowBytes;
+            p.set_path = g_combine_policy == 2 ||
+                         (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets && (!rows_ok || big_rows));
         }
     }
     // K splits for the 32-row (decode) GEMMs and the f32 kernels, whose output

@@ -182,21 +182,22 @@ def test_moe_status_symbol_rejects_without_launch():
 
 @pytest.mark.parametrize("T, H, I, E, k, path, kernel", [
     # Nomic (H 768): the down GEMM's 3 column tiles never fill the CUs twice on
-    # the two-per-CU tile, so the 256x256 tile throughout; pairs up to 1.4 row
-    # tiles per expert set
+    # the two-per-CU tile, so the 256x256 tile throughout; its pair rows
+    # (T*k*H 16-bit values) stay below 256 MiB, so the pair path throughout
     (1024, 768, 3072, 8, 2, "pairs", 7),
     (4096, 768, 3072, 8, 2, "pairs", 7),
-    (8192, 768, 3072, 8, 2, "pairs", 7),
-    (12288, 768, 3072, 8, 2, "expert-set", 7),
-    (32768, 768, 3072, 8, 2, "expert-set", 7),
+    (12288, 768, 3072, 8, 2, "pairs", 7),
+    (32768, 768, 3072, 8, 2, "pairs", 7),
     # Qwen3-30B-A3B (H 2048, 128 experts): two-per-CU 128x256 tile below 1024
     # rows per expert; (E+1)^k keys too many for the expert-set path
     (1024, 2048, 768, 128, 8, "pairs", 14),
     (4096, 2048, 768, 128, 8, "pairs", 14),
     (16384, 2048, 768, 128, 8, "pairs", 7),
-    # Qwen3 (H 4096): expert sets from half a row tile per set (T >= 3584)
-    (2048, 4096, 1536, 8, 2, "pairs", 7),
-    (4096, 4096, 1536, 8, 2, "expert-set", 7),
+    # Qwen3 (H 4096): expert sets once the pair rows reach 256 MiB (T >= 16384)
+    (4096, 4096, 1536, 8, 2, "pairs", 7),
+    (8192, 4096, 1536, 8, 2, "pairs", 7),
+    (16384, 4096, 1536, 8, 2, "expert-set", 7),
+    (32768, 4096, 1536, 8, 2, "expert-set", 7),
 ])
 def test_default_path_and_kernel(T, H, I, E, k, path, kernel):
     """The host's default combine path and GEMM kernel (no GPU needed)."""
