@@ -452,3 +452,14 @@ def test_pair_path_output_alignment(offset):
     assert_close(from_dev(out).astype(np.float64), want, RTOL[dt], f"output offset {offset}")
     # the elements around the output are untouched
     assert float(buf[:offset].abs().sum()) == 0.0 and float(buf[offset + T * H:].abs().sum()) == 0.0
+
+
+# ---- pair path on the prefill kernels with k = 4: each pair's weighted row is
+# stored once and a token's k rows are summed (no atomics)
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt, mt, act", [(O.BF16, O.QWEN3, O.SILU), (O.F16, O.NOMIC, O.GELU)])
+def test_pair_rows_four_experts_per_token(dt, mt, act):
+    T, H, I, E, k = 2048, 128, 64, 16, 4
+    assert candle_moe.fused_moe_path(T, H, I, E, k, dt) == "pairs"
+    assert candle_moe.fused_moe_kernel(T, H, I, E, k, dt) != 12  # not the 32-row decode kernel
+    check_case(T, H, I, E, k, dt, mt, act=act, seed=71, rows=list(range(0, T, 61)))
