@@ -108,6 +108,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_set_tile_policy.restype = i32
         L.candle_moe_fused_moe_path.argtypes = [i32] * 5 + [u32]
         L.candle_moe_fused_moe_path.restype = i32
+        L.candle_moe_fused_moe_path_ex.argtypes = [i32] * 5 + [u32, u32]
+        L.candle_moe_fused_moe_path_ex.restype = i32
         L.candle_moe_profile_begin.argtypes = []
         L.candle_moe_profile_begin.restype = i32
         L.candle_moe_profile_begin_slots.argtypes = [u32]
@@ -347,11 +349,11 @@ def set_combine_policy(policy: int) -> None:
     check(lib().candle_moe_set_combine_policy(int(policy)))
 
 
-(TILE_AUTO, TILE_128, TILE_256, TILE_LDS_256, TILE_LDS_256x128, TILE_LDS_128, TILE_LDS_256K64, TILE_W8, TILE_W8K32,
- TILE_PINGPONG, TILE_W8K32_SPREAD, TILE_K32_SPREAD, TILE_ROWS32, TILE_256x128_OCC2, TILE_128x256_OCC2,
- TILE_F32_ROWS32, TILE_F32_128) = range(17)
-_TILE_ROWS = {0: 64, 1: 128, 2: 256, 3: 256, 4: 256, 5: 128, 6: 256, 7: 256, 8: 256, 9: 256, 10: 256, 11: 256, 12: 32,
-              13: 256, 14: 128, 15: 32, 16: 128}
+# GEMM kernel codes of candle_moe_set_tile_policy (include/candle_moe.h)
+TILE_AUTO, TILE_128, TILE_LDS_128, TILE_W8, TILE_ROWS32, TILE_128x256_OCC2, TILE_F32_ROWS32, TILE_F32_128 = \
+    0, 1, 5, 7, 12, 14, 15, 16
+TILE_CODES = (TILE_AUTO, TILE_128, TILE_LDS_128, TILE_W8, TILE_ROWS32, TILE_128x256_OCC2, TILE_F32_ROWS32, TILE_F32_128)
+_TILE_ROWS = {0: 64, 1: 128, 5: 128, 7: 256, 12: 32, 14: 128, 15: 32, 16: 128}
 
 
 def set_tile_policy(policy: int) -> None:
@@ -359,21 +361,34 @@ def set_tile_policy(policy: int) -> None:
     check(lib().candle_moe_set_tile_policy(int(policy)))
 
 
-def fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> str:
+def _path_code(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type):
+    return lib().candle_moe_fused_moe_path_ex(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k,
+                                              dtype_code, moe_type)
+
+
+def fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type=0) -> str:
     """Name of the path fused_moe takes for these sizes under the current policy."""
-    code = lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
+    code = _path_code(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type)
     return PATH_NAMES[code if code < 0 else code & 3]
 
 
-def fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> int:
+def fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type=0) -> int:
     """GEMM kernel code (TILE_*) fused_moe uses for these sizes (-1 if invalid)."""
-    code = lib().candle_moe_fused_moe_path(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
-    return -1 if code < 0 else code >> 2
+    code = _path_code(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type)
+    return -1 if code < 0 else (code >> 2) & 0x3f
 
 
-def fused_moe_tile(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code) -> int:
+def fused_moe_pair_rows(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code,
+                        moe_type=0) -> bool:
+    """True when the pair path stores each pair's row and sums a token's k rows
+    (False: f32 atomics into an accumulator, or not the pair path)."""
+    code = _path_code(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type)
+    return code >= 0 and bool(code & (1 << 8))
+
+
+def fused_moe_tile(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type=0) -> int:
     """Block-tile rows of the GEMM kernels fused_moe uses for these sizes (64 for SIMT)."""
-    k = fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code)
+    k = fused_moe_kernel(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k, dtype_code, moe_type)
     return 0 if k < 0 else _TILE_ROWS[k]
 
 

@@ -8,12 +8,18 @@
 //   activation and routing weight fused, rows written in token-set order)
 //   -> GEMM2 over K = k*I per expert set, added once into the output.
 //  pair path (everything else):
-//   pair grouping -> GEMM1 (activation fused) -> zero f32 accumulator
-//   -> GEMM2 (routing weight and coalesced f32 atomic scatter-add fused)
-//   -> finalize (output += accumulator, rounded once).
+//   pair grouping -> GEMM1 (activation fused) -> GEMM2 with the routing
+//   weight fused, then either
+//    * pair rows (16-bit prefill kernels): each pair's weighted row stored
+//      in the dtype, then a pass that sums a token's k rows in f32 in slot
+//      order and adds them to the output (rounded once), or
+//    * f32 atomics (32-row decode kernels, f32 kernels, and pair rows that
+//      would exceed kRowsMaxBytes): coalesced atomic adds into an f32
+//      [T, H] accumulator that the gate/up launch clears, then finalize
+//      (output += accumulator, rounded once).
 // Workspace (256-byte aligned pieces): offsets[E+2], per-block counts,
 // sorted pair ids, row-tile table, intermediate [T*k, I] in the input dtype
-// and the f32 accumulator [T, H].
+// and the pair rows [T*k, H] (dtype) or the f32 accumulator [T, H].
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -163,13 +169,18 @@ struct Layout {
     size_t inter, acc, partial, counters, total;
 };
 
-// 0: choose per call; 1: always the pair path (f32 atomics); 2: the
-// expert-set path whenever the shape allows it.
+// 0: choose per call; 1: always the pair path (pair rows or f32 atomics,
+// by kernel); 2: the expert-set path whenever the shape allows it.
 // Pair-row bytes (T*k*H 16-bit values) from which the expert-set path is
 // preferred over the pair path's row stores and k-row sums.
 constexpr double kSetMinRowBytes = 256.0 * 1024 * 1024;
+// Largest pair-row buffer (T*k*H 16-bit values) the pair path stores; beyond
+// it the down GEMM adds into the f32 [T, H] accumulator with atomics instead
+// (k*H*2 bytes per token against H*4), which bounds the workspace of shapes
+// whose expert sets are too many for the expert-set path (large k and E).
+constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
 static int g_combine_policy = 0;
-// 0: choose the MFMA tile per call; kTile128 / kTile256: force it.
+// 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
 
 static long long set_tiles_max(const Problem& p) {
@@ -228,8 +239,13 @@ static Layout make_layout(const Problem& p) {
     return L;
 }
 
+// aligned16: input and weights start on 16-byte boundaries (the MFMA and f32
+// tiled kernels read them with 16-byte loads; otherwise the scalar kernel
+// runs). out16: so does the output (the expert-set down GEMM stores straight
+// into it, 8 bytes at a time; otherwise the pair path, whose last pass
+// handles any alignment).
 static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
-                         Problem& p, bool aligned16 = true) {
+                         Problem& p, bool aligned16 = true, bool out16 = true) {
     if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
     if (H < 1 || I < 1)
         return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: hidden_dim and intermediate_dim must be >= 1 (got %d, %d)", H, I);
@@ -244,7 +260,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens * num_selected_experts exceeds 2^31-1");
     p.T = T; p.H = H; p.I = I; p.E = E; p.k = k; p.act = act; p.moe_type = (int)moe_type; p.dtype = (int)dtype;
     p.P = P;
-    p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H);
+    p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H) && aligned16;
     // Default MFMA kernel, by rows per touched expert (measured on MI355X
     // over T = 1 .. 32768 of the Qwen3, Qwen3-30B and Nomic shapes):
     //  * at most 32 (decode): the GEMMs stream each touched expert's weights
@@ -297,7 +313,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // 404 us at T=12288).
     p.set_path = false;
     p.nkeys = 0;
-    if (p.mfma && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
+    if (p.mfma && out16 && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
         long long nk = 1;
         for (int j = 0; j < k && nk <= kSetMaxKeys; ++j) nk *= (E + 1);
         if (nk <= kSetMaxKeys) {
@@ -311,7 +327,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             // are large: Qwen3 T=4096 / 8192 pairs 454 / 792 against sets 484 /
             // 830 us, T=32768 (537 MB of rows) sets 2346 against 2499 us;
             // Nomic T=12288 / 32768 pairs 377 / 859 against 390 / 899 us.
-            const bool rows_ok = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong && p.dtype != kF32;
+            const bool rows_ok = p.mfma && is_lds_cfg(p.cfg) && p.dtype != kF32;
             const bool big_rows = (double)P * H * 2.0 >= (double)kSetMinRowBytes;
             p.set_path = g_combine_policy == 2 ||
                          (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets && (!rows_ok || big_rows));
@@ -330,7 +346,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     //    host's count from the expected tiles, up to ~512 workgroups and 16
     //    splits (they gain from more than one round: Nomic T=512 f32 fc1
     //    136 us against 150-190 us with the device's one-round choice).
-    p.lds_family = p.mfma && is_lds_cfg(p.cfg) && p.cfg != kPingPong;
+    p.lds_family = p.mfma && is_lds_cfg(p.cfg);
     p.fused_clear_ok = p.lds_family || is_f32_cfg(p.cfg);
     // Pair path on the LDS-DMA kernels (16-bit): the down GEMM stores each
     // pair's weighted row once and a row-contiguous pass sums a token's k
@@ -339,7 +355,8 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // Qwen3-30B-A3B shapes). Deterministic for every k. Not for the 32-row
     // decode kernels, whose few atomics cost less than the k-row pass
     // (Qwen3-30B-A3B T=16: 90 against 94 us).
-    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32;
+    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 &&
+                  (double)P * H * 2.0 <= kRowsMaxBytes;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
     p.split1 = p.split2 = 1;
@@ -611,7 +628,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
     Problem p;
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const bool aligned16 = a16(x) && a16(gate) && a16(up) && a16(down);
-    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16);
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out));
     if (rc) return rc;
     rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
     if (rc) return rc;
@@ -639,11 +656,16 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
 }
 
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
-    // the kernel choice may depend on the operands' alignment: enough for either
-    Problem p, q;
-    if (check_problem(T, H, I, E, k, 0, 0, dtype, p, true)) return 0;
-    if (check_problem(T, H, I, E, k, 0, 0, dtype, q, false)) return 0;
-    return std::max(make_layout(p).total, make_layout(q).total);
+    // the kernel choice may depend on the operands' alignment and on the
+    // moe_type (the gate/up and fc1 tiles differ in width): enough for each
+    size_t most = 0;
+    for (uint32_t mt = 0; mt < 2; ++mt)
+        for (int al = 0; al < 2; ++al) {
+            Problem p;
+            if (check_problem(T, H, I, E, k, 0, mt, dtype, p, al != 0)) return 0;
+            most = std::max(most, make_layout(p).total);
+        }
+    return most;
 }
 
 }  // namespace cm
@@ -798,18 +820,27 @@ int candle_moe_set_combine_policy(int policy) {
 }
 
 int candle_moe_set_tile_policy(int policy) {
-    if (policy < 0 || policy >= cm::kNumTileCfgs)
-        return cm::set_error(CANDLE_MOE_ERR_INVALID, "tile policy must be in [0, %d)", cm::kNumTileCfgs);
+    if (policy < 0 || policy >= cm::kNumTileCfgs || !cm::is_shipped_cfg(policy))
+        return cm::set_error(CANDLE_MOE_ERR_INVALID,
+                             "tile policy must be one of 0 (auto), 1, 5, 7, 12, 14, 15, 16 (got %d)", policy);
     cm::g_tile_policy = policy;
     return CANDLE_MOE_OK;
 }
 
+int candle_moe_fused_moe_path_ex(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                 int num_selected_experts, uint32_t dtype, uint32_t moe_type) {
+    cm::Problem p;
+    if (cm::check_problem(num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts, 0, moe_type,
+                          dtype, p))
+        return -1;
+    return (p.set_path ? 2 : (p.mfma ? 1 : 0)) | (p.cfg << 2) | (p.rows_path ? (1 << 8) : 0);
+}
+
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype) {
-    cm::Problem p;
-    if (cm::check_problem(num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts, 0, 0, dtype, p))
-        return -1;
-    return (p.set_path ? 2 : (p.mfma ? 1 : 0)) | (p.cfg << 2);
+    const int c = candle_moe_fused_moe_path_ex(num_tokens, hidden_dim, intermediate_dim, num_experts,
+                                               num_selected_experts, dtype, 0);
+    return c < 0 ? c : (c & 0xff);
 }
 
 int candle_moe_profile_begin(void) {

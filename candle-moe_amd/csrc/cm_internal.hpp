@@ -114,39 +114,43 @@ struct GemmArgs {
 constexpr int kTailMaxSplit = 8;
 constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter splits lose to the fixup)
 
-// Kernel shapes. kTileSimt: 64x64 SIMT; kTile128 / kTile256: MFMA kernels
-// with 128x128 / 256x256 block tiles (the grouping tile table must be built
-// with the same row tile, tile_rows()).
-// kLds*: the LDS-DMA kernels (moe_gemm_lds.hip): 256x256 with BK=32 and 4
-// stages, 256x128 BK=64 3 stages, 128x128 BK=64 4 stages, 256x256 BK=64
-// 2 stages.
-// kLds256w8 / kLds256w8k32: 256x256 with 8 waves (2 per SIMD), BK=64 2 stages
-// / BK=32 4 stages.
-// kPingPong: 256x256, 8 waves in two groups that alternate MFMA and memory
-// phases (moe_gemm_pp.hip).
-// kLds256w8k32s / kLds256k32s: 256x256, BK=32, 4 stages, 8 / 4 waves, with
-// each K tile's DMA spread over the k16 steps of the tile before it.
-// kLdsRows32: 32x256 block tile, 4 waves side by side along N, BK=64,
-// 4 stages: few rows per expert (decode), bound by streaming the weights.
+// Kernel shapes (the codes of candle_moe_set_tile_policy; the missing codes
+// belonged to measured variants that are not shipped and are rejected).
+// kTileSimt: 64x64 SIMT (f32 and shapes the MFMA kernels do not take).
+// kTile128: register-staged MFMA kernel, 128x128 block tile (operands beyond
+//   the 2 GiB range of the LDS-DMA kernels' buffer offsets).
+// LDS-DMA MFMA kernels (moe_gemm_lds.hip):
+//   kLds128: 128x128, 4 waves, BK 64, 4 stages;
+//   kLds256w8: 256x256, 8 waves (2 per SIMD), BK 64, 2 stages (prefill);
+//   kLdsRows32: 32x256, 4 waves side by side along N, BK 64, 4 stages: few
+//     rows per expert (decode), bound by streaming the weights;
+//   kLds128x256o2: 128x256, 4 waves, BK 32, 3 stages, two workgroups per CU.
+// f32 vector-FMA kernels (moe_gemm_f32.hip): kF32Rows32 (32x128 block tile),
+//   kF32Tile128 (128x128).
+// The grouping's tile table must be built with the kernel's row tile,
+// tile_rows().
 enum TileCfg : int {
-    kTileSimt = 0, kTile128 = 1, kTile256 = 2, kLds256 = 3, kLds256x128 = 4, kLds128 = 5, kLds256k64 = 6,
-    kLds256w8 = 7, kLds256w8k32 = 8, kPingPong = 9, kLds256w8k32s = 10, kLds256k32s = 11, kLdsRows32 = 12,
-    kLds256x128o2 = 13, kLds128x256o2 = 14, kF32Rows32 = 15, kF32Tile128 = 16
+    kTileSimt = 0, kTile128 = 1, kLds128 = 5, kLds256w8 = 7, kLdsRows32 = 12, kLds128x256o2 = 14,
+    kF32Rows32 = 15, kF32Tile128 = 16
 };
-constexpr int kNumTileCfgs = 17;
+constexpr int kNumTileCfgs = 17;  // codes are < kNumTileCfgs
+inline bool is_shipped_cfg(int cfg) {
+    return cfg == kTileSimt || cfg == kTile128 || cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 ||
+           cfg == kLds128x256o2 || cfg == kF32Rows32 || cfg == kF32Tile128;
+}
 inline bool is_f32_cfg(int cfg) { return cfg == kF32Rows32 || cfg == kF32Tile128; }
 inline int tile_rows(int cfg) {
     if (cfg == kLdsRows32 || cfg == kF32Rows32) return 32;
-    if (cfg == kF32Tile128) return 128;
-    return (cfg == kTileSimt) ? 64 : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds128x256o2) ? 128 : 256);
+    if (cfg == kTileSimt) return 64;
+    if (cfg == kLds256w8) return 256;
+    return 128;  // kTile128, kLds128, kLds128x256o2, kF32Tile128
 }
 inline int tile_cols(int cfg) {
-    if (is_f32_cfg(cfg)) return 128;
-    return (cfg == kTileSimt) ? 64
-                              : ((cfg == kTile128 || cfg == kLds128 || cfg == kLds256x128 || cfg == kLds256x128o2) ? 128
-                                                                                                                    : 256);
+    if (cfg == kTileSimt) return 64;
+    if (cfg == kLds256w8 || cfg == kLdsRows32 || cfg == kLds128x256o2) return 256;
+    return 128;  // kTile128, kLds128, f32 kernels
 }
-inline bool is_lds_cfg(int cfg) { return cfg >= kLds256 && !is_f32_cfg(cfg); }
+inline bool is_lds_cfg(int cfg) { return cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 || cfg == kLds128x256o2; }
 // Workgroups of a launch over at most `tiles` output tiles: with adaptive K
 // splits live tiles * splits stays within split_target when it splits.
 inline long long split_grid(long long tiles, const GemmArgs& a) {
@@ -157,10 +161,7 @@ inline long long split_grid(long long tiles, const GemmArgs& a) {
 // K tile of the LDS-DMA kernels
 inline int tile_bk(int cfg) {
     if (is_f32_cfg(cfg)) return 16;
-    return (cfg == kLds256 || cfg == kLds256w8k32 || cfg == kLds256w8k32s || cfg == kLds256k32s ||
-            cfg == kLds256x128o2 || cfg == kLds128x256o2)
-               ? 32
-               : 64;
+    return cfg == kLds128x256o2 ? 32 : 64;
 }
 
 bool mfma_supported(int dtype, int K, int N);
@@ -168,7 +169,6 @@ bool mfma_supported(int dtype, int K, int N);
 int gemm_tile_cols(int mode, int cfg);
 hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
-hipError_t launch_moe_gemm_pp(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
 

@@ -1,5 +1,5 @@
-// Device helpers shared by the LDS-DMA grouped GEMMs (moe_gemm_lds.hip,
-// moe_gemm_pp.hip): buffer resources, global->LDS DMA, explicit waits,
+// Device helpers of the LDS-DMA grouped GEMMs (moe_gemm_lds.hip): buffer
+// resources, global->LDS DMA, explicit waits,
 // LDS swizzles, XCD-aware tile order and the per-tile epilogues.
 #pragma once
 

@@ -639,14 +639,11 @@ template <int DT, int MODE>
 static hipError_t launch_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     const int nwg = a.m_tiles_max * a.n_tiles;
     if (nwg <= 0) return hipSuccess;
-    if (cfg == kTile128 || cfg == kTile256) {
+    if (cfg == kTile128) {
         if constexpr (DT == kF32) {
             return hipErrorInvalidValue;
         } else {
-            if (cfg == kTile256)
-                hipLaunchKernelGGL((moe_mfma_gemm<DT, 256, 256, MODE>), dim3(nwg), dim3(256), 0, stream, a);
-            else
-                hipLaunchKernelGGL((moe_mfma_gemm<DT, 128, 128, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((moe_mfma_gemm<DT, 128, 128, MODE>), dim3(nwg), dim3(256), 0, stream, a);
         }
     } else {
         if constexpr (MODE == kDownSet || MODE == kFc2Set) {

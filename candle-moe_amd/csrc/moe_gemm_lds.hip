@@ -29,7 +29,7 @@ namespace cm {
 
 using namespace lds;
 
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, bool SPREAD = false, int WGM = 2, int OCC = 1>
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, int WGM = 2, int OCC = 1>
 __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // NW waves in WGM rows: 4 in a 2x2 layout (one per SIMD), 8 in 2x4 (two
     // per SIMD, so one wave's MFMAs cover the other's LDS, DMA and VALU work),
@@ -300,21 +300,13 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     };
     // KSTEPS k16 steps per stage; the fragments of step kk+1 are read while
     // the MFMAs of step kk run (two register sets).
-    // SPREAD: the DMA of the tile NST-1 ahead (stage ds, k0 dk; ds < 0: none)
-    // is issued in KSTEPS slices, one after each k16 step's MFMAs, so that a
-    // K tile's 64 KB reach the L2 at an even rate instead of in one burst
-    // that stalls the issuing waves.
-    constexpr int PER_STEP = (LOADS + KSTEPS - 1) / KSTEPS;
-    // Otherwise (8 waves): the waves of row group 1 issue the whole DMA of
-    // the next tile after their first k16 step's MFMAs (ds >= 0 only for
-    // them), so that the two waves sharing a SIMD do not both stall on the
-    // memory pipeline right after the barrier (2 % on the prefill GEMMs;
-    // issuing later leaves the DMA too little time before the next barrier).
+    // 8 waves: the waves of row group 1 issue the whole DMA of the next tile
+    // after their first k16 step's MFMAs (ds >= 0 only for them), so that the
+    // two waves sharing a SIMD do not both stall on the memory pipeline right
+    // after the barrier (2 % on the prefill GEMMs; issuing later leaves the
+    // DMA too little time before the next barrier).
     auto dma_slice = [&](int ds, int dk, int step) {
-        if constexpr (SPREAD) {
-            if (ds >= 0) issue_range(ds, dk, step * PER_STEP, (step + 1) * PER_STEP);
-            __builtin_amdgcn_sched_barrier(0);
-        } else if constexpr (NW == 8) {
+        if constexpr (NW == 8) {
             if (step == 0 && ds >= 0) issue_range(ds, dk, 0, LOADS);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -323,9 +315,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // group) reads no fragments and issues no MFMAs; it still issues its DMA
     // share and meets every barrier. On a half-empty tile this leaves the
     // matrix core of each SIMD to the other wave.
-    // (Not in the 4-wave 256x256 kernels, whose 256 accumulators leave no
-    // registers for the second code path.)
-    const bool rows_live = MB * NB > 8 || wm * WM < m_valid;
+    const bool rows_live = wm * WM < m_valid;
     auto compute = [&](int stage, int ds, int dk) {
         if (!rows_live) {
 #pragma unroll
@@ -403,7 +393,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     const int kt0 = min(nk_all, ks * per_split);
     const int nk = min(nk_all, kt0 + per_split) - kt0;
 
-    if constexpr (!SPREAD && NW == 4 && !GATHER) {
+    if constexpr (NW == 4 && !GATHER) {
         // 4-wave down / fc2 kernels: hand-over one k16 step early. The
         // barrier of tile kt+1 sits before the MFMAs of tile kt's last k16
         // step, whose fragments are already in registers, so the MFMAs issued
@@ -496,13 +486,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         wait_lgkm0();
         block_barrier();
         const int ahead = kt + NST - 1;
-        if constexpr (SPREAD) {
-            compute(kt % NST, ahead < nk ? ahead % NST : -1, (kt0 + ahead) * BK);
-        } else {
-            const bool late = NW == 8 && wm == 1;  // row group 1 issues after its first k16 step
-            if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
-            compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
-        }
+        const bool late = NW == 8 && wm == 1;  // row group 1 issues after its first k16 step
+        if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
+        compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
     }
     }
 
@@ -535,41 +521,19 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
         return hipErrorInvalidValue;
     } else {
         switch (cfg) {
-            case kLds256:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 4, MODE>), dim3(nwg), dim3(256), 0, stream, a);
-                break;
-            case kLds256x128:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 128, 64, 3, 4, MODE>), dim3(nwg), dim3(256), 0, stream, a);
-                break;
             case kLds128:
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 128, 64, 4, 4, MODE>), dim3(nwg), dim3(256), 0, stream, a);
-                break;
-            case kLds256k64:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 4, MODE>), dim3(nwg), dim3(256), 0, stream, a);
                 break;
             case kLds256w8:
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
                 break;
-            case kLds256w8k32:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
-                break;
-            case kLds256w8k32s:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 8, MODE, true>), dim3(nwg), dim3(512), 0, stream, a);
-                break;
-            case kLds256k32s:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 32, 4, 4, MODE, true>), dim3(nwg), dim3(256), 0, stream, a);
-                break;
             case kLdsRows32:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, false, 1>), dim3(nwg), dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0, stream, a);
                 break;
             // two workgroups per CU (72 KB of LDS, at most 256 VGPRs each): one
             // workgroup's barrier and DMA issue overlap the other's MFMAs
-            case kLds256x128o2:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 128, 32, 3, 4, MODE, false, 2, 2>), dim3(nwg), dim3(256), 0,
-                                   stream, a);
-                break;
             case kLds128x256o2:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 256, 32, 3, 4, MODE, false, 2, 2>), dim3(nwg), dim3(256), 0,
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 256, 32, 3, 4, MODE, 2, 2>), dim3(nwg), dim3(256), 0,
                                    stream, a);
                 break;
             default:
@@ -595,10 +559,6 @@ static hipError_t launch_lds_dt(int mode, int cfg, const GemmArgs& a, hipStream_
 }
 
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
-    if (cfg == kPingPong) {
-        if (mode == kDownRows || mode == kFc2Rows) return hipErrorInvalidValue;
-        return launch_moe_gemm_pp(mode, dtype, a, stream);
-    }
     if (dtype == kBF16) return launch_lds_dt<kBF16>(mode, cfg, a, stream);
     if (dtype == kF16) return launch_lds_dt<kF16>(mode, cfg, a, stream);
     return hipErrorInvalidValue;

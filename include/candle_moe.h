@@ -99,7 +99,8 @@ int candle_moe_fused_moe_status(const void* input, const void* gate_weights, con
                                 uint32_t dtype, void* stream);
 
 /* Caller-provided workspace: bytes needed by candle_moe_fused_moe_ws for
- * these sizes (0 when the arguments are invalid). */
+ * these sizes, for either moe_type and any operand alignment (0 when the
+ * arguments are invalid). */
 size_t candle_moe_fused_moe_workspace_size(int num_tokens, int hidden_dim, int intermediate_dim,
                                            int num_experts, int num_selected_experts,
                                            uint32_t dtype);
@@ -132,26 +133,31 @@ const char* candle_moe_profile_slot_name(int slot);
  *     intermediate_dim % 64 == 0, (E+1)^k <= 1024, k <= 8). */
 int candle_moe_set_combine_policy(int policy);
 /* GEMM kernel of fused_moe (process-wide): 0 = choose per call (default);
- * register-staged MFMA kernels 1 = 128x128, 2 = 256x256 block tiles;
- * LDS-DMA MFMA kernels 3 = 256x256 (BK 32), 4 = 256x128, 5 = 128x128,
- * 6 = 256x256 (BK 64, 4 waves), 7 = 256x256 (8 waves), 8 = 256x256 (8 waves,
- * BK 32), 9 = 256x256 (8 waves alternating MFMA and memory phases),
- * 10 / 11 = 256x256 BK 32 with the DMA spread over the K loop, 8 / 4 waves,
+ * 1 = register-staged MFMA kernel, 128x128 block tile (taken by default only
+ *     when an operand exceeds the 2 GiB range of the LDS-DMA kernels);
+ * LDS-DMA MFMA kernels: 5 = 128x128, 7 = 256x256 (8 waves),
  * 12 = 32x256 (default when experts get <= 32 rows on average),
- * 13 / 14 = 256x128 / 128x256 (BK 32, two workgroups per CU). By default 5
- * is taken for <= 128 rows per expert where the 256x256 tile would give few
- * workgroups, 14 for < 1024 rows per expert with hidden_dim <= 2048 when the
- * down GEMM has at least two 128x256 tiles per CU, else 7.
+ * 14 = 128x256 (BK 32, two workgroups per CU). By default 5 is taken for
+ * <= 128 rows per expert where the 256x256 tile would give few workgroups,
+ * 14 for < 1024 rows per expert with hidden_dim <= 2048 when the down GEMM
+ * has at least two 128x256 tiles per CU, else 7.
  * f32 (vector FMA): 15 = 32x128 tile, 16 = 128x128 tile, both with K splits
  * when the tiles are few; by default 15 for <= 32 rows per expert, else 16
  * (the scalar 64x64 kernel 0 when hidden_dim or intermediate_dim is not a
- * multiple of 4 or an operand is not 16-byte aligned). */
+ * multiple of 4 or an operand is not 16-byte aligned).
+ * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
 int candle_moe_set_tile_policy(int policy);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
  * bits 2 and up: the GEMM kernel (policy code above); -1 = invalid sizes. */
 int candle_moe_fused_moe_path(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                               int num_selected_experts, uint32_t dtype);
+/* The same for a given moe_type (candle_moe_fused_moe_path answers for
+ * moe_type 0, Qwen3; the Nomic fc1 tile can differ), with bit 8 set when the
+ * pair path stores pair rows and sums them per token (clear: f32 atomics
+ * into an accumulator and a finalize pass). */
+int candle_moe_fused_moe_path_ex(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                 int num_selected_experts, uint32_t dtype, uint32_t moe_type);
 
 /* Router GEMM fused with topk-softmax (no counterpart symbol in the
  * reference; its callers compute the logits with a separate candle matmul,

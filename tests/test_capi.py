@@ -180,29 +180,51 @@ def test_moe_status_symbol_rejects_without_launch():
     assert L.candle_moe_fused_moe_status(*args, 0, 64, 256, 8, 2, 0, 0, 1, None) == cm.CANDLE_MOE_OK
 
 
-@pytest.mark.parametrize("T, H, I, E, k, path, kernel", [
-    # Nomic (H 768): the down GEMM's 3 column tiles never fill the CUs twice on
-    # the two-per-CU tile, so the 256x256 tile throughout; its pair rows
-    # (T*k*H 16-bit values) stay below 256 MiB, so the pair path throughout
-    (1024, 768, 3072, 8, 2, "pairs", 7),
-    (4096, 768, 3072, 8, 2, "pairs", 7),
-    (12288, 768, 3072, 8, 2, "pairs", 7),
-    (32768, 768, 3072, 8, 2, "pairs", 7),
+@pytest.mark.parametrize("T, H, I, E, k, mt, path, kernel, rows", [
+    # Nomic (H 768, moe_type 1): the down GEMM's 3 column tiles never fill the
+    # CUs twice on the two-per-CU tile; few rows per expert take the 128x128
+    # tile, the rest the 256x256 tile; its pair rows (T*k*H 16-bit values)
+    # stay below 256 MiB, so the pair path with pair rows throughout
+    (16, 768, 3072, 8, 2, 1, "pairs", 12, False),
+    (512, 768, 3072, 8, 2, 1, "pairs", 5, True),
+    (1024, 768, 3072, 8, 2, 1, "pairs", 7, True),
+    (4096, 768, 3072, 8, 2, 1, "pairs", 7, True),
+    (12288, 768, 3072, 8, 2, 1, "pairs", 7, True),
+    (32768, 768, 3072, 8, 2, 1, "pairs", 7, True),
     # Qwen3-30B-A3B (H 2048, 128 experts): two-per-CU 128x256 tile below 1024
     # rows per expert; (E+1)^k keys too many for the expert-set path
-    (1024, 2048, 768, 128, 8, "pairs", 14),
-    (4096, 2048, 768, 128, 8, "pairs", 14),
-    (16384, 2048, 768, 128, 8, "pairs", 7),
+    (1024, 2048, 768, 128, 8, 0, "pairs", 14, True),
+    (4096, 2048, 768, 128, 8, 0, "pairs", 14, True),
+    (16384, 2048, 768, 128, 8, 0, "pairs", 7, True),
+    # pair rows beyond 2 GiB: f32 atomics into the [T, H] accumulator instead
+    (131072, 2048, 768, 128, 8, 0, "pairs", 7, False),
     # Qwen3 (H 4096): expert sets once the pair rows reach 256 MiB (T >= 16384)
-    (4096, 4096, 1536, 8, 2, "pairs", 7),
-    (8192, 4096, 1536, 8, 2, "pairs", 7),
-    (16384, 4096, 1536, 8, 2, "expert-set", 7),
-    (32768, 4096, 1536, 8, 2, "expert-set", 7),
+    (8, 4096, 1536, 8, 2, 0, "pairs", 12, False),
+    (512, 4096, 1536, 8, 2, 0, "pairs", 5, True),
+    (4096, 4096, 1536, 8, 2, 0, "pairs", 7, True),
+    (8192, 4096, 1536, 8, 2, 0, "pairs", 7, True),
+    (16384, 4096, 1536, 8, 2, 0, "expert-set", 7, False),
+    (32768, 4096, 1536, 8, 2, 0, "expert-set", 7, False),
 ])
-def test_default_path_and_kernel(T, H, I, E, k, path, kernel):
+def test_default_path_and_kernel(T, H, I, E, k, mt, path, kernel, rows):
     """The host's default combine path and GEMM kernel (no GPU needed)."""
-    assert cm.fused_moe_path(T, H, I, E, k, 1) == path
-    assert cm.fused_moe_kernel(T, H, I, E, k, 1) == kernel
+    assert cm.fused_moe_path(T, H, I, E, k, 1, mt) == path
+    assert cm.fused_moe_kernel(T, H, I, E, k, 1, mt) == kernel
+    assert cm.fused_moe_pair_rows(T, H, I, E, k, 1, mt) == rows
+    if mt == 0:  # the original query answers for Qwen3
+        code = cm.lib().candle_moe_fused_moe_path(T, H, I, E, k, 1)
+        assert code == (cm.lib().candle_moe_fused_moe_path_ex(T, H, I, E, k, 1, 0) & 0xff)
+
+
+def test_tile_policy_accepts_only_shipped_kernels():
+    for code in cm.TILE_CODES:
+        cm.set_tile_policy(code)
+    cm.set_tile_policy(0)
+    for code in (2, 3, 4, 6, 8, 9, 10, 11, 13, 17, -1):
+        with pytest.raises(cm.CandleMoeError) as e:
+            cm.set_tile_policy(code)
+        assert e.value.code == cm.CANDLE_MOE_ERR_INVALID
+    cm.set_tile_policy(0)
 
 
 def test_workspace_size():
@@ -210,14 +232,19 @@ def test_workspace_size():
     small = L.candle_moe_fused_moe_workspace_size(32, 64, 256, 8, 2, 1)
     big = L.candle_moe_fused_moe_workspace_size(32768, 4096, 1536, 8, 2, 1)
     assert 0 < small < big
-    # the expert-set path needs the bf16 intermediate [T*k, I] only ...
+    # the expert-set path needs the bf16 intermediate [T*k, I] only; the size
+    # also covers operands off a 16-byte boundary (scalar kernel, pair path
+    # with the f32 accumulator [T, H])
     assert cm.fused_moe_path(32768, 4096, 1536, 8, 2, 1) == "expert-set"
-    assert 65536 * 1536 * 2 <= big < 65536 * 1536 * 2 + 32768 * 4096 * 4
+    assert 65536 * 1536 * 2 + 32768 * 4096 * 4 <= big < 65536 * 1536 * 2 + 32768 * 4096 * 4 + (64 << 20)
     # ... the pair path also the f32 accumulator [T, H]
     assert cm.fused_moe_path(4096, 2048, 768, 128, 8, 1) == "pairs"
     q30 = L.candle_moe_fused_moe_workspace_size(4096, 2048, 768, 128, 8, 1)
     assert q30 >= 32768 * 768 * 2 + 4096 * 2048 * 4
     assert L.candle_moe_fused_moe_workspace_size(32, 64, 256, 0, 2, 1) == 0
+    # an upper bound for both moe_types (Nomic's fc1 tile may differ from gate/up's)
+    nomic = L.candle_moe_fused_moe_workspace_size(512, 768, 3072, 8, 2, 1)
+    assert nomic >= 1024 * 3072 * 2 + 1024 * 768 * 2
     # workspace variant: too-small workspace is refused before anything runs
     rc = L.candle_moe_fused_moe_ws(*([ctypes.c_void_p(256)] * 7), 32, 64, 256, 8, 2, 0, 0, 1,
                                    ctypes.c_void_p(256), 16, None)
