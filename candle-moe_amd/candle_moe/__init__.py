@@ -102,6 +102,10 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_workspace_size.restype = sz
         L.candle_moe_fused_moe_ws.argtypes = moe_args + [vp, sz, vp]
         L.candle_moe_fused_moe_ws.restype = i32
+        L.candle_moe_fused_moe_noalloc.argtypes = moe_args + [vp]
+        L.candle_moe_fused_moe_noalloc.restype = i32
+        L.candle_moe_fused_moe_noalloc_scratch_bytes.argtypes = []
+        L.candle_moe_fused_moe_noalloc_scratch_bytes.restype = sz
         L.candle_moe_set_combine_policy.argtypes = [i32]
         L.candle_moe_set_combine_policy.restype = i32
         L.candle_moe_set_tile_policy.argtypes = [i32]

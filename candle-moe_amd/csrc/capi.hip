@@ -655,6 +655,64 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
                    out, overwrite, reinterpret_cast<char*>(w->ptr), s);
 }
 
+// ----------------------------------------------- fused MoE without allocation
+// Scratch of candle_moe_fused_moe_noalloc: a file-scope device array, one per
+// GPU the library is loaded on, held until the process ends. In host code
+// `scratch` names a host-side stand-in, not a device address: the device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current, and only that address is ever handed to kernels.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_of_current_device(void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "fused_moe_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(CANDLE_MOE_ERR_UNSUPPORTED, "fused_moe_noalloc: device ordinal %d beyond %d", dev,
+                         kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                   "fused_moe_noalloc: hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return CANDLE_MOE_OK;
+}
+
+int fused_moe_noalloc_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
+                           const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
+                           uint32_t dtype, void* stream) {
+    clear_error();
+    Problem p;
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    const bool aligned16 = a16(x) && a16(gate) && a16(up) && a16(down);
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out));
+    if (rc) return rc;
+    rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
+    if (rc) return rc;
+    if (T == 0) return CANDLE_MOE_OK;
+    const Layout L = make_layout(p);
+    if (L.total > kNoAllocScratchBytes)
+        return set_error(CANDLE_MOE_ERR_WORKSPACE,
+                         "fused_moe_noalloc: this call needs %zu bytes of scratch; the library holds %zu per device "
+                         "(use fused_moe or candle_moe_fused_moe_ws for larger calls)",
+                         L.total, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_of_current_device(&ws);
+    if (rc) return rc;
+    // every piece of the layout that must start at zero (split-K arrival
+    // counters, the f32 accumulator) is cleared by this call's own kernels
+    return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
+                   out, false, reinterpret_cast<char*>(ws), reinterpret_cast<hipStream_t>(stream));
+}
+
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
     // the kernel choice may depend on the operands' alignment and on the
     // moe_type (the gate/up and fc1 tiles differ in width): enough for each
@@ -713,6 +771,18 @@ int candle_moe_fused_moe_status(const void* input, const void* gate_weights, con
                               num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
                               activation_type, moe_type, dtype, nullptr, 0, true, false, stream);
 }
+
+int candle_moe_fused_moe_noalloc(const void* input, const void* gate_weights, const void* up_weights,
+                                 const void* down_weights, const void* routing_weights, const void* expert_indices,
+                                 void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                 int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+                                 void* stream) {
+    return cm::fused_moe_noalloc_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices,
+                                      output, num_tokens, hidden_dim, intermediate_dim, num_experts,
+                                      num_selected_experts, activation_type, moe_type, dtype, stream);
+}
+
+size_t candle_moe_fused_moe_noalloc_scratch_bytes(void) { return cm::kNoAllocScratchBytes; }
 
 size_t candle_moe_fused_moe_workspace_size(int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
                                            int num_selected_experts, uint32_t dtype) {

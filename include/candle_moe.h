@@ -114,6 +114,27 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
                             int num_selected_experts, int activation_type, uint32_t moe_type,
                             uint32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* fused_moe that allocates nothing, for callers that cannot allocate (code
+ * under HIP graph capture, serving loops that must not call hipMalloc,
+ * harnesses that forbid it). No counterpart in the reference, whose fused_moe
+ * allocates its workspace per call (/root/reference/kernels/moe.cu:570,770).
+ * Same arguments and result as candle_moe_fused_moe_status (output is added
+ * into); the workspace is a fixed device array inside the library, one per
+ * GPU, of candle_moe_fused_moe_noalloc_scratch_bytes() bytes (32 MiB: decode
+ * and small prefill batches, e.g. Qwen3 H4096 I1536 E8 k2 up to ~1400 tokens),
+ * held until the process ends. A call that needs more is rejected with
+ * CANDLE_MOE_ERR_WORKSPACE before anything is launched. All calls on one GPU
+ * share that array: calls that may overlap on one GPU (other streams, other
+ * host threads without ordering) race and must be serialised by the caller.
+ * Each call clears what must start at zero; nothing else carries over. */
+int candle_moe_fused_moe_noalloc(const void* input, const void* gate_weights, const void* up_weights,
+                                 const void* down_weights, const void* routing_weights,
+                                 const void* expert_indices, void* output, int num_tokens,
+                                 int hidden_dim, int intermediate_dim, int num_experts,
+                                 int num_selected_experts, int activation_type, uint32_t moe_type,
+                                 uint32_t dtype, void* stream);
+size_t candle_moe_fused_moe_noalloc_scratch_bytes(void);
+
 /* Per-kernel timing for benchmarks: between begin and end, every internal
  * launch is bracketed by HIP events on the caller's stream. end() waits for
  * those events and returns, per slot, the summed milliseconds and the number

@@ -279,3 +279,18 @@ def test_grouping_entry_point_rejects_without_launch():
     assert L.candle_moe_group_pairs(None, 4, 5000, None, None, None, 0, None) == cm.CANDLE_MOE_ERR_INVALID
     assert L.candle_moe_group_pairs(ctypes.c_void_p(256), 4, 8, ctypes.c_void_p(256), ctypes.c_void_p(256),
                                     ctypes.c_void_p(256), 16, None) == cm.CANDLE_MOE_ERR_WORKSPACE
+
+
+def test_noalloc_rejects_without_launch():
+    # candle_moe_fused_moe_noalloc refuses a call whose workspace exceeds the
+    # library's fixed scratch before touching the GPU
+    L = cm.lib()
+    assert L.candle_moe_fused_moe_noalloc_scratch_bytes() == 32 << 20
+    p = ctypes.c_void_p(256)
+    rc = L.candle_moe_fused_moe_noalloc(p, p, p, p, p, p, p, 8192, 4096, 1536, 8, 2, 0, 0, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_WORKSPACE
+    assert "fused_moe_noalloc" in cm.last_error() and "33554432" in cm.last_error()
+    assert L.candle_moe_fused_moe_noalloc(None, None, None, None, None, None, None, 16, 64, 256, 8, 2, 0, 0, 1,
+                                          None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_fused_moe_noalloc(None, None, None, None, None, None, None, 0, 64, 256, 8, 2, 0, 0, 1,
+                                          None) == cm.CANDLE_MOE_OK
