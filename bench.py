@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
+    ap.add_argument("--no-router-shapes", dest="router_shapes", action="store_false",
+                    help="skip the topk-softmax config-2 shapes reported next to the MoE step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the warmup, run 3 plain copy kernels of MIB MiB (read MIB, write MIB; "
                          "the reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -194,6 +196,12 @@ def main():
         rms = float(ref.pow(2).mean().sqrt())
         if not torch.allclose(gout.float(), ref, rtol=2e-2, atol=2e-2 * rms):
             graph_ms = None
+    # the drop-in path: what the reference's Rust caller runs per call
+    # (Tensor::zeros of the output, /root/reference/src/lib.rs:296, then the
+    # fused_moe symbol adding into it, ffi.rs:35), timed the same way
+    dropin = bench_dropin(torch, L, x, gate, up, down, topk_w, topk_i, wl, act, args)
+    router = bench_router_shapes(torch, cm, dev, args) if args.router_shapes else None
+
     c = 6 if qwen3 else 4
     flops = float(T) * k * c * H * I
     tflops = flops / (ms_per_step * 1e-3) / 1e12
@@ -236,6 +244,8 @@ def main():
         "topk_softmax_gbs": round(topk_bytes / (topk_us * 1e-6) / 1e9, 1) if topk_us else None,
         "kernels_us": kernels,
         "graph_ms_per_step": round(graph_ms, 4) if graph_ms else None,
+        "dropin_fused_moe": dropin,
+        "topk_softmax_config2": router,
         "kernels_note": "HIP-event averages per launch: gemm_gate_up from the timed steps (the only kernel "
                         "bracketed there), the others from an untimed pass of up to 10 steps with every "
                         "launch bracketed",
@@ -292,7 +302,10 @@ def cpu_baseline(torch, x, gate, up, down, topk_w, topk_i, wl, S):
     G, U, D = host(gate), host(up), host(down)
     w = topk_w[:S].cpu().numpy()
     idx = topk_i[:S].cpu().numpy().astype(np.uint32)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    host_cpus = len(os.sched_getaffinity(0))
+    # every CPU this process may run on, unless the environment limits the
+    # OpenMP threads (the GPU boxes set OMP_NUM_THREADS to their per-GPU share)
+    threads = min(host_cpus, int(os.environ.get("OMP_NUM_THREADS", "0")) or host_cpus)
     act = {"silu": O.SILU, "gelu": O.GELU, "relu": O.RELU}[wl["act"]]
     t0 = time.perf_counter()
     O.fused_moe(xs, G, U, D, w, idx, E=wl["E"], k=wl["k"], act=act, moe_type=wl["moe_type"], dtype=dt,
@@ -304,11 +317,91 @@ def cpu_baseline(torch, x, gate, up, down, topk_w, topk_i, wl, S):
         "value": round(flops / dt_s / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
+        "host_cpus": host_cpus,
+        "host_cpus_online": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
         "sample": f"{'all' if S == wl['T'] else 'first'} {S} of {wl['T']} tokens with all {wl['E']} experts' "
                   f"weights; candle-native per-expert loop (oracle/oracle.c, per-op {wl['dtype']} rounding); "
-                  f"{dt_s:.2f} s wall on {threads} threads",
+                  f"{dt_s:.2f} s wall on {threads} OpenMP threads (one per CPU of this process's affinity set "
+                  f"of {host_cpus}, capped by OMP_NUM_THREADS)",
     }
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def bench_dropin(torch, L, x, gate, up, down, topk_w, topk_i, wl, act, args):
+    """ms per call of the reference caller's sequence: a zeroed [T, H] output
+    (torch.zeros, a fill kernel) then the raw fused_moe symbol, which adds into
+    it; warm library workspace, same inputs as the step."""
+    T, H = x.shape
+    I = gate.shape[2]
+    dt = {"f16": 0, "bf16": 1, "f32": 2}[wl["dtype"]]
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call():
+        out = torch.zeros((T, H), dtype=x.dtype, device=x.device)
+        L.fused_moe(p(x), p(gate), p(up), p(down), p(topk_w), p(topk_i), p(out), T, H, I, wl["E"], wl["k"],
+                    int(act), wl["moe_type"], dt, stream)
+        return out
+
+    for _ in range(max(2, args.warmup)):
+        call()
+    torch.cuda.synchronize()
+    n = max(5, args.steps // 2)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        call()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / n
+    return {"ms_per_call": round(ms, 4),
+            "note": "torch.zeros([T,H]) + the raw fused_moe symbol accumulating into it (the reference caller's "
+                    "per-call work); the step above uses FusedMoE::forward, whose last kernel writes every output "
+                    "element instead"}
+
+
+def bench_router_shapes(torch, cm, dev, args):
+    """topk-softmax at BASELINE config 2 (f32 logits N(0,1); [32768,8] k2,
+    [32768,64] k6, [32768,128] k8 and the skewed [32768,8] k2 with a per-expert
+    N(0, 2) bias): GPU µs per call from 50 calls captured in one graph and
+    replayed, rotating over logits buffers that exceed the 256 MB last-level
+    cache (cold), and the achieved GB/s of T*E*4 + T*k*12 bytes."""
+    res = {}
+    for name, T, E, k, skew in [("32768x8k2", 32768, 8, 2, 0.0), ("32768x64k6", 32768, 64, 6, 0.0),
+                                ("32768x128k8", 32768, 128, 8, 0.0), ("32768x8k2_skewed", 32768, 8, 2, 2.0)]:
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + E)
+        nbuf = max(1, (512 << 20) // (T * E * 4))
+        bias = torch.randn((E,), generator=g, device=dev) * skew
+        logits = [torch.randn((T, E), generator=g, device=dev) + bias[None, :] for _ in range(nbuf)]
+        w = torch.empty((T, k), device=dev)
+        i = torch.empty((T, k), dtype=torch.int32, device=dev)
+        ei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        for _ in range(3):
+            cm.apply_topk_softmax_inplace(logits[0], w, i, ei)
+        torch.cuda.synchronize()
+        cm.apply_topk_softmax_inplace(logits[49 % nbuf], w, i, ei)
+        ref = (w.clone(), i.clone(), ei.clone())
+        gus = graph_us(torch, lambda: [cm.apply_topk_softmax_inplace(logits[s % nbuf], w, i, ei) for s in range(50)],
+                       50, 20, lambda: torch.equal(w, ref[0]) and torch.equal(i, ref[1]) and torch.equal(ei, ref[2]))
+        nbytes = T * E * 4 + T * k * 12
+        res[name] = {"us": round(gus, 2) if gus else None,
+                     "gbs": round(nbytes / (gus * 1e-6) / 1e9, 1) if gus else None,
+                     "hbm_frac": round(nbytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4) if gus else None}
+        del logits
+    return res
 
 
 def graph_us(torch, calls, ncalls, reps, check):

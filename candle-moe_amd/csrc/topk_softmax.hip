@@ -103,6 +103,47 @@ __device__ __forceinline__ void group_argmax(float& v, int& i) {
     if constexpr (LPR >= 64) argmax_step<32>(v, i);
 }
 
+// f32(e^d) for an f32 d <= 0: the f64 exponential rounded once to f32, as the
+// CPU restatement computes it ((float)exp((double)d)). Reduction by ln 2
+// (n = rint(d / ln 2), r = d - n ln 2 with ln 2 split in a 40-bit head and a
+// tail, both steps exact but the last rounding), e^r = 1 + r (1 + r/2 + ... +
+// r^11/12!) by Horner in fused multiply-adds, times 2^n. This exact sequence
+// of IEEE f64 operations (every step an explicit fma, no contraction left to
+// the compiler) gives the same f32 as glibc's exp for every one of the
+// 1,120,927,745 f32 values in [-104, 0] (checked exhaustively); below -104 the
+// result rounds to +0. NaN stays NaN.
+// The coefficients sit in a mutable __constant__ array so that the compiler
+// loads them into scalar registers once instead of rebuilding each 64-bit
+// literal in vector registers at every use.
+__constant__ double kExpCoef[15] = {
+    0x1.71547652b82fep+0,
+    0x1.62e42fefa4000p-1,
+    -0x1.8432a1b0e2634p-43,
+    0x1.1eed8eff8d898p-29,
+    0x1.ae64567f544e4p-26,
+    0x1.27e4fb7789f5cp-22,
+    0x1.71de3a556c734p-19,
+    0x1.a01a01a01a01ap-16,
+    0x1.a01a01a01a01ap-13,
+    0x1.6c16c16c16c17p-10,
+    0x1.1111111111111p-7,
+    0x1.5555555555555p-5,
+    0x1.5555555555555p-3,
+    0x1.0000000000000p-1,
+    0x1.0000000000000p+0};  // 1/ln2, ln2 head, ln2 tail, 1/12! .. 1/1!
+__device__ __forceinline__ float exp_f32_f64(float d) {
+#pragma clang fp contract(off)
+    const double x = (double)d;
+    const double n = __builtin_rint(x * kExpCoef[0]);
+    double r = __builtin_fma(-n, kExpCoef[1], x);
+    r = __builtin_fma(-n, kExpCoef[2], r);
+    double s = kExpCoef[3];
+#pragma unroll
+    for (int i = 4; i < 15; ++i) s = __builtin_fma(r, s, kExpCoef[i]);
+    const double y = __builtin_ldexp(__builtin_fma(s, r, 1.0), (int)n);
+    return d < -104.0f ? 0.0f : (float)y;
+}
+
 template <int VPT, int INDT>
 __device__ __forceinline__ void load_row_values(const void* __restrict__ logits, long long row, int E,
                                                 int e0, bool full, float (&x)[VPT]) {
@@ -133,17 +174,155 @@ __device__ __forceinline__ void load_row_values(const void* __restrict__ logits,
     }
 }
 
+// Selection keys: (p, expert) in the order p descending, then the lower
+// expert, as one unsigned 64-bit value: high word the bits of p (p >= +0, so
+// its bits order like its value), low word ~expert. Slots past E get p = +0
+// and an expert >= E, so they order after every real expert (also those
+// with p = 0), and k <= E never selects them.
+__device__ __forceinline__ uint64_t sel_key(float p, int e) {
+    return ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(~(uint32_t)e);
+}
+// a, b -> (max, min)
+__device__ __forceinline__ void key_cx(uint64_t& a, uint64_t& b) {
+    const bool s = b > a;
+    const uint64_t hi = s ? b : a, lo = s ? a : b;
+    a = hi;
+    b = lo;
+}
+// Sorting networks (descending), checked exhaustively over 0/1 inputs in the
+// tests: 1 comparator for 2 keys, 5 for 4, 19 for 8.
+template <int N>
+__device__ __forceinline__ void sort_keys(uint64_t (&k)[N]) {
+    if constexpr (N == 2) {
+        key_cx(k[0], k[1]);
+    } else if constexpr (N == 4) {
+        key_cx(k[0], k[1]); key_cx(k[2], k[3]);
+        key_cx(k[0], k[2]); key_cx(k[1], k[3]);
+        key_cx(k[1], k[2]);
+    } else if constexpr (N == 8) {
+        key_cx(k[0], k[2]); key_cx(k[1], k[3]); key_cx(k[4], k[6]); key_cx(k[5], k[7]);
+        key_cx(k[0], k[4]); key_cx(k[1], k[5]); key_cx(k[2], k[6]); key_cx(k[3], k[7]);
+        key_cx(k[0], k[1]); key_cx(k[2], k[3]); key_cx(k[4], k[5]); key_cx(k[6], k[7]);
+        key_cx(k[2], k[4]); key_cx(k[3], k[5]);
+        key_cx(k[1], k[4]); key_cx(k[3], k[6]);
+        key_cx(k[1], k[2]); key_cx(k[3], k[4]); key_cx(k[5], k[6]);
+    } else {
+        static_assert(N == 1, "sort_keys: 1, 2, 4 or 8 keys");
+    }
+}
+// The lanes of `mask` (a wave-wide lane mask) take b, the others keep a: one
+// v_cndmask_b32 per 32-bit word. (Written as a plain select inside the
+// head-drop shift below, the compiler turns `pop ? key[q+1] : key[q]` into
+// an indexed read key[q + pop] and expands that into a compare chain per
+// slot.)
+__device__ __forceinline__ uint64_t key_take(uint64_t a, uint64_t b, uint64_t mask) {
+    uint32_t lo, hi;
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(lo) : "v"((uint32_t)a), "v"((uint32_t)b), "s"(mask));
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(hi) : "v"((uint32_t)(a >> 32)), "v"((uint32_t)(b >> 32)), "s"(mask));
+    return ((uint64_t)hi << 32) | lo;
+}
+// 32-bit keys: compare-exchange by max / min, the same networks.
+__device__ __forceinline__ void key32_cx(uint32_t& a, uint32_t& b) {
+    const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+    a = hi;
+    b = lo;
+}
+template <int N>
+__device__ __forceinline__ void sort_keys32(uint32_t (&k)[N]) {
+    if constexpr (N == 2) {
+        key32_cx(k[0], k[1]);
+    } else if constexpr (N == 4) {
+        key32_cx(k[0], k[1]); key32_cx(k[2], k[3]);
+        key32_cx(k[0], k[2]); key32_cx(k[1], k[3]);
+        key32_cx(k[1], k[2]);
+    } else if constexpr (N == 8) {
+        key32_cx(k[0], k[2]); key32_cx(k[1], k[3]); key32_cx(k[4], k[6]); key32_cx(k[5], k[7]);
+        key32_cx(k[0], k[4]); key32_cx(k[1], k[5]); key32_cx(k[2], k[6]); key32_cx(k[3], k[7]);
+        key32_cx(k[0], k[1]); key32_cx(k[2], k[3]); key32_cx(k[4], k[5]); key32_cx(k[6], k[7]);
+        key32_cx(k[2], k[4]); key32_cx(k[3], k[5]);
+        key32_cx(k[1], k[4]); key32_cx(k[3], k[6]);
+        key32_cx(k[1], k[2]); key32_cx(k[3], k[4]); key32_cx(k[5], k[6]);
+    } else {
+        static_assert(N == 1, "sort_keys32: 1, 2, 4 or 8 keys");
+    }
+}
+__device__ __forceinline__ uint32_t key_take32(uint32_t a, uint32_t b, uint64_t mask) {
+    uint32_t r;
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+    return r;
+}
+// max(v, v of the partner lane) in one DPP-modified v_max_u32 for the
+// steps inside a row of 16 lanes (the s_nop covers the wait states between a
+// VALU write of v and its DPP read, which the compiler does not track across
+// inline asm).
+template <int M>
+__device__ __forceinline__ uint32_t key32_max_step(uint32_t v) {
+    if constexpr (M == 1 || M == 2 || M == 4 || M == 8) {
+        uint32_t r;
+        if constexpr (M == 1)
+            asm volatile("s_nop 1\n\tv_max_u32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+                         : "=v"(r) : "v"(v));
+        else if constexpr (M == 2)
+            asm volatile("s_nop 1\n\tv_max_u32_dpp %0, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+                         : "=v"(r) : "v"(v));
+        else if constexpr (M == 4)
+            asm volatile("s_nop 1\n\tv_max_u32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf"
+                         : "=v"(r) : "v"(v));
+        else
+            asm volatile("s_nop 1\n\tv_max_u32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xf"
+                         : "=v"(r) : "v"(v));
+        return r;
+    } else {
+        uint32_t a, b;
+        lane_pair<M>(v, a, b);
+        return a > b ? a : b;
+    }
+}
+template <int LPR>
+__device__ __forceinline__ uint32_t group_key32_max(uint32_t v) {
+    if constexpr (LPR >= 2) v = key32_max_step<1>(v);
+    if constexpr (LPR >= 4) v = key32_max_step<2>(v);
+    if constexpr (LPR >= 8) v = key32_max_step<4>(v);
+    if constexpr (LPR >= 16) v = key32_max_step<8>(v);
+    if constexpr (LPR >= 32) v = key32_max_step<16>(v);
+    if constexpr (LPR >= 64) v = key32_max_step<32>(v);
+    return v;
+}
+// Largest key of an LPR-lane group (every lane of the group gets it).
+template <int M>
+__device__ __forceinline__ uint64_t key_max_step(uint64_t v) {
+    uint32_t al, bl, ah, bh;
+    lane_pair<M>((uint32_t)v, al, bl);
+    lane_pair<M>((uint32_t)(v >> 32), ah, bh);
+    const uint64_t a = ((uint64_t)ah << 32) | al, b = ((uint64_t)bh << 32) | bl;
+    return b > a ? b : a;
+}
+template <int LPR>
+__device__ __forceinline__ uint64_t group_key_max(uint64_t v) {
+    if constexpr (LPR >= 2) v = key_max_step<1>(v);
+    if constexpr (LPR >= 4) v = key_max_step<2>(v);
+    if constexpr (LPR >= 8) v = key_max_step<4>(v);
+    if constexpr (LPR >= 16) v = key_max_step<8>(v);
+    if constexpr (LPR >= 32) v = key_max_step<16>(v);
+    if constexpr (LPR >= 64) v = key_max_step<32>(v);
+    return v;
+}
+
 // Softmax over one token's E logits held by a group of LPR lanes (lane g of
 // the group: experts e0 + q*ESTR, q < VPT, -inf past E), then the top k in
-// descending order, ties to the lower index; lane j % LPR writes output j.
+// descending order, ties to the lower index; output j of a row is written by
+// lane j of its group (k <= LPR, one coalesced store per output tensor after
+// the k passes) or lane j % LPR right away (k > LPR).
 // R independent tokens per lane group at once (row r's logits in x[r]): their
-// cross-lane exchanges interleave, which hides the swizzle latencies when a
+// cross-lane exchanges interleave, which hides the exchange latencies when a
 // SIMD holds a single wave.
+// Selection (VPT <= 8): each lane sorts its VPT keys once; pass j takes the
+// group's largest head key and the lane that owned it drops its head.
 template <int VPT, int LPR, int OUTDT, int ESTR, int R>
 __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int e0, int g, int E, int k, int T,
                                                   const long long (&row)[R], const bool (&valid)[R],
                                                   void* __restrict__ wout, uint32_t* __restrict__ iout,
-                                                  uint32_t* __restrict__ eiout) {
+                                                  uint32_t* __restrict__ eiout, float* s_row = nullptr) {
     float m[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -162,50 +341,157 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const float d = x[r][j] - m[r];
-            p[r][j] = (e0 + j * ESTR < E) ? (float)exp((double)d) : 0.0f;
+            const float ex = exp_f32_f64(d);  // every slot: straight-line code
+            p[r][j] = (e0 + j * ESTR < E) ? ex : 0.0f;
             s[r] += (double)p[r][j];
         }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) s[r] = group_sum<LPR>(s[r]);
+    // p = e / S in f32: e * (1 / S) with both steps in f64 and one rounding to
+    // f32 is the correctly rounded quotient (its error, < 2^-52 relative,
+    // stays below the distance of any f32 quotient from a rounding midpoint)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const float S = (float)s[r];
+        const double inv = 1.0 / (double)(float)s[r];
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) p[r][j] = (e0 + j * ESTR < E) ? p[r][j] / S : -1.0f;
+        for (int j = 0; j < VPT; ++j) p[r][j] = (float)((double)p[r][j] * inv);
     }
 
     typedef typename Elem<OUTDT>::storage WS;
     WS* wo = reinterpret_cast<WS*>(wout);
-    for (int j = 0; j < k; ++j) {
-        float bv[R];
-        int bi[R];
+    auto put = [&](long long rw, int j, float v, int e) {
+        const long long o = rw * (long long)k + j;
+        wo[o] = Elem<OUTDT>::from_f32(v);
+        iout[o] = (uint32_t)e;
+        eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)rw;
+    };
+    // Fast selection on 32-bit keys (R == 1 with an LDS row buffer, k <= LPR): the key
+    // of expert e is p's bits with the low IB bits replaced by MASK - e, plus
+    // one (so that 0 stays below every expert). Keys order as (upper bits of
+    // p, lower expert), and where the upper bits of two keys differ that is
+    // the order of (p, lower expert) itself. k + 1 passes over the lanes'
+    // sorted keys give the first k + 1 keys; if their upper bits strictly
+    // decrease, the first k are the exact top k in order (every other expert
+    // has smaller upper bits than the k-th). Otherwise (near-equal p, e.g.
+    // planted ties) the wave redoes the row with the exact 64-bit keys below.
+    // The weights are the exact p, read back from the row buffer in LDS.
+    bool exact_done = false;
+    if constexpr (R == 1 && VPT <= 8 && LPR * VPT <= 256) {
+        if (s_row != nullptr && k <= LPR) {  // lane j of the group writes output j
+            constexpr int IB = (LPR * VPT <= 2) ? 1 : 32 - __builtin_clz(LPR * VPT - 1);
+            constexpr uint32_t MASK = (1u << IB) - 1u;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            bv[r] = p[r][0];
-            bi[r] = e0;
+            for (int q = 0; q < VPT; ++q) s_row[e0 + q * ESTR] = p[0][q];
+            // (read back by other lanes of this wave after the passes: LDS
+            // runs one wave's instructions in order; keep the compiler from
+            // moving the reads above the writes)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            uint32_t key[VPT];
 #pragma unroll
-            for (int q = 1; q < VPT; ++q) {
-                const bool take = p[r][q] > bv[r];
-                bv[r] = take ? p[r][q] : bv[r];
-                bi[r] = take ? e0 + q * ESTR : bi[r];
+            for (int q = 0; q < VPT; ++q)
+                key[q] = ((__float_as_uint(p[0][q]) | MASK) - (uint32_t)(e0 + q * ESTR)) + 1u;
+            sort_keys32<VPT>(key);
+            uint32_t mine = 0u, prev = 0xffffffffu;
+            bool ordered = true;
+            for (int j = 0; j <= k; ++j) {
+                const uint32_t best = group_key32_max<LPR>(key[0]);
+                // (once only zero keys are left every lane pops a zero: harmless)
+                const uint64_t pop = __builtin_amdgcn_ballot_w64(key[0] == best);
+#pragma unroll
+                for (int q = 0; q + 1 < VPT; ++q) key[q] = key_take32(key[q], key[q + 1], pop);
+                key[VPT - 1] = key_take32(key[VPT - 1], 0u, pop);
+                const uint32_t up = (best - 1u) | MASK;  // upper bits of p (0 keys: none left)
+                if (j < k || k < E) ordered = ordered && (best == 0u ? j == k : up < prev);
+                prev = up;
+                mine = g == j ? best : mine;
+            }
+            // one wave-wide decision: a row that needs the exact path sends
+            // its whole wave there
+            if (__builtin_amdgcn_ballot_w64(!ordered) == 0ull) {
+                exact_done = true;
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (valid[0] && g < k) {
+                    const int e = (int)(MASK - ((mine - 1u) & MASK));
+                    put(row[0], g, s_row[e], e);
+                }
             }
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) group_argmax<LPR>(bv[r], bi[r]);
+    }
+    if (exact_done) return;
+    if constexpr (VPT <= 8) {
+        uint64_t key[R][VPT];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
-            for (int q = 0; q < VPT; ++q) p[r][q] = (e0 + q * ESTR == bi[r]) ? -2.0f : p[r][q];
+            for (int q = 0; q < VPT; ++q) key[r][q] = sel_key(p[r][q], e0 + q * ESTR);
+            sort_keys<VPT>(key[r]);
         }
+        const bool gather = k <= LPR;  // lane j keeps output j
+        float ov[R];
+        int oi[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (valid[r] && g == (j % LPR)) {
-                const long long o = row[r] * (long long)k + j;
-                wo[o] = Elem<OUTDT>::from_f32(bv[r]);
-                iout[o] = (uint32_t)bi[r];
-                eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)row[r];
+            ov[r] = 0.0f;
+            oi[r] = 0;
+        }
+        for (int j = 0; j < k; ++j) {
+            uint64_t best[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) best[r] = group_key_max<LPR>(key[r][0]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                // the owner of the best key drops its head
+                const uint64_t pop = __builtin_amdgcn_ballot_w64(key[r][0] == best[r]);
+#pragma unroll
+                for (int q = 0; q + 1 < VPT; ++q) key[r][q] = key_take(key[r][q], key[r][q + 1], pop);
+                key[r][VPT - 1] = key_take(key[r][VPT - 1], 0ull, pop);
+                const float bv = __uint_as_float((uint32_t)(best[r] >> 32));
+                const int bi = (int)~(uint32_t)best[r];
+                if (gather) {
+                    ov[r] = g == j ? bv : ov[r];
+                    oi[r] = g == j ? bi : oi[r];
+                } else if (valid[r] && g == (j % LPR)) {
+                    put(row[r], j, bv, bi);
+                }
             }
+        }
+        if (gather) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (valid[r] && g < k) put(row[r], g, ov[r], oi[r]);
+        }
+    } else {
+        // many experts per lane: k argmax passes over the lane's values
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) p[r][j] = (e0 + j * ESTR < E) ? p[r][j] : -1.0f;
+        for (int j = 0; j < k; ++j) {
+            float bv[R];
+            int bi[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                bv[r] = p[r][0];
+                bi[r] = e0;
+#pragma unroll
+                for (int q = 1; q < VPT; ++q) {
+                    const bool take = p[r][q] > bv[r];
+                    bv[r] = take ? p[r][q] : bv[r];
+                    bi[r] = take ? e0 + q * ESTR : bi[r];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) group_argmax<LPR>(bv[r], bi[r]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int q = 0; q < VPT; ++q) p[r][q] = (e0 + q * ESTR == bi[r]) ? -2.0f : p[r][q];
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (valid[r] && g == (j % LPR)) put(row[r], j, bv[r], bi[r]);
         }
     }
 }
@@ -213,15 +499,16 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
 template <int VPT, int LPR, int OUTDT, int ESTR = 1>
 __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
                                                    long long row, bool valid, void* __restrict__ wout,
-                                                   uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout) {
+                                                   uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout,
+                                                   float* s_row = nullptr) {
     const float(&xr)[1][VPT] = reinterpret_cast<const float(&)[1][VPT]>(x);
     const long long rr[1] = {row};
     const bool vr[1] = {valid};
-    softmax_topk_rows<VPT, LPR, OUTDT, ESTR, 1>(xr, e0, g, E, k, T, rr, vr, wout, iout, eiout);
+    softmax_topk_rows<VPT, LPR, OUTDT, ESTR, 1>(xr, e0, g, E, k, T, rr, vr, wout, iout, eiout, s_row);
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
-__global__ __launch_bounds__(128) void topk_softmax_kernel(const void* __restrict__ logits,
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restrict__ logits,
                                                           void* __restrict__ wout,
                                                           uint32_t* __restrict__ iout,
                                                           uint32_t* __restrict__ eiout, int T, int E,
@@ -239,13 +526,18 @@ __global__ __launch_bounds__(128) void topk_softmax_kernel(const void* __restric
     float x[VPT];
     load_row_values<VPT, INDT>(logits, r, E, e0, full, x);
 
-    softmax_topk_group<VPT, LPR, OUTDT>(x, e0, g, E, k, T, row, valid, wout, iout, eiout);
+    // one LDS row of p per lane group (the fast selection reads the weights
+    // of the chosen experts back from it; written and read by one wave)
+    constexpr bool FAST = VPT <= 8 && LPR * VPT <= 256 && LPR > 1;
+    __shared__ float s_p[FAST ? 256 / LPR : 1][FAST ? LPR * VPT : 1];
+    softmax_topk_group<VPT, LPR, OUTDT>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
+                                        FAST ? s_p[threadIdx.x / LPR] : nullptr);
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
 static hipError_t launch_cfg(const void* logits, void* w, uint32_t* idx, uint32_t* ei, int T, int E,
                              int k, hipStream_t stream) {
-    constexpr int BLOCK = 128;
+    constexpr int BLOCK = 256;
     const long long threads = (long long)T * LPR;
     const unsigned grid = (unsigned)cdivll(threads, BLOCK);
     const int aligned = ((uintptr_t)logits % 16) == 0;

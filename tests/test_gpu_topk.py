@@ -139,3 +139,49 @@ def test_deterministic_reruns():
     b = run_router(g, 8)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+def test_exp_and_division_bit_exact_over_the_whole_range():
+    # Two experts per row, logits (0, d): the row sum has one order, so every
+    # weight must equal the oracle's bit for bit -- p1 = f32(exp(d)) / S over
+    # d from 0 down past the f32 underflow at -103.97, denormals included,
+    # and -inf (weight +0).
+    d = np.concatenate([-np.logspace(-8, np.log10(120.0), 200_000), np.linspace(-104.5, -86.0, 50_000),
+                        [0.0, -0.0, -1e-45, -103.9721, -103.97, -104.0, -np.inf]]).astype(np.float32)
+    g = np.stack([np.zeros_like(d), d], axis=1)
+    w, i, _ = run_router(g, 2)
+    w_ref, i_ref, _ = O.topk_softmax(g, 2)
+    assert np.array_equal(i, i_ref)
+    assert np.array_equal(w.view(np.uint32), w_ref.view(np.uint32)), \
+        f"{int((w.view(np.uint32) != w_ref.view(np.uint32)).sum())} weights differ in their bits"
+    assert (w[-1] == np.array([1.0, 0.0], np.float32)).all()
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (8, 2)])
+def test_weights_bit_exact_when_one_lane_holds_the_row(E, k):
+    # up to 8 experts one lane holds the whole row and sums it in the oracle's
+    # order: weights bit-exact as well
+    g = router_inputs(32768, E, seed=95 + E)
+    w, i, _ = run_router(g, k)
+    w_ref, i_ref, _ = O.topk_softmax(g, k)
+    assert np.array_equal(i, i_ref)
+    assert np.array_equal(w.view(np.uint32), w_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("E,k", [(16, 2), (32, 4), (64, 6), (128, 8), (256, 8)])
+def test_near_ties_take_the_exact_selection(E, k):
+    # Rows whose leading logits are equal or 1-2 ulps apart give probabilities
+    # that agree in all but their last bits, where the 32-bit selection keys
+    # cannot order them: those waves redo the rows with 64-bit keys. Rows of
+    # both kinds share waves here, every 5th row has near-ties.
+    T = 4096
+    g = router_inputs(T, E, seed=97 + E)
+    rng = np.random.default_rng(E)
+    for t in range(0, T, 5):
+        top = rng.choice(E, size=min(E, k + 2), replace=False)
+        base = np.float32(2.5 + rng.random())
+        vals = [base, base, np.nextafter(base, np.float32(-10)), np.nextafter(base, np.float32(10)),
+                np.nextafter(np.nextafter(base, np.float32(-10)), np.float32(-10))]
+        for n, e in enumerate(top):
+            g[t, e] = vals[n % len(vals)]
+    check_router(g, k)
