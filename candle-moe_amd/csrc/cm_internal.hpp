@@ -55,7 +55,8 @@ GroupJob pair_grouping_job(const uint32_t* idx, long long P, int E, int BM, cons
 GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, int BM, const GroupingBufs& b,
                           int32_t* pair_dest);
 size_t a256_bytes(size_t x);  // x rounded up to 256 bytes
-// The pair grouping and optionally the token grouping, in at most three launches.
+// The pair grouping and optionally the token grouping: one launch when both
+// have at most kGroupSmallMax items, else two (histogram, scan + scatter).
 hipError_t launch_groupings(const GroupJob& pairs, const GroupJob* tokens, hipStream_t stream);
 
 // ----------------------------------------------------------- grouped GEMM

@@ -9,89 +9,110 @@
 // deterministic), and the multi-block path scans per-block counts instead of
 // aliasing counts and offsets (/root/reference/kernels/preprocessing.cuh:296-298).
 //
-// Up to kGroupSmallMax items one workgroup does everything (small_body).
-// Beyond that, three phases, no host synchronisation:
-//   1. hist_body   : each workgroup histograms kGroupChunk items in LDS
-//   2. scan_body   : one workgroup turns the per-block counts into per-block
-//                    bases (one wave-wide scan per bin), the bin offsets and
-//                    the tile table
-//   3. scatter_body: each workgroup re-reads its chunk and ranks items
-//                    stably: 64-lane peer masks from ballots inside a wave,
-//                    per-wave running counts in LDS, one barrier to turn the
-//                    per-wave counts into bases
-// The same code groups tokens by their expert set (TOK = true) for the
-// expert-set down projection. The pair grouping and the token grouping share
-// three launches (grouping_hist_k, grouping_mid_k, grouping_scatter_k), each
-// workgroup serving one of the two jobs; a small job runs whole in the
-// middle launch, so decode groupings take one launch.
+// Up to kGroupSmallMax items one workgroup does everything (small_body), one
+// launch. Beyond that, two launches, no host synchronisation:
+//   1. hist_body   : each workgroup histograms kGroupChunk items in LDS and
+//                    stores its per-bin counts
+//   2. scatter_body: each workgroup stages every block's counts in LDS (all
+//                    loads in flight together), sums each bin over all blocks
+//                    and over the blocks before its own (the bin totals give
+//                    the offsets by one block-wide scan, which workgroup 0
+//                    also writes out with the tile table), then ranks its
+//                    items stably -- 64-lane peer masks from ballots inside a
+//                    wave, per-wave running counts in LDS, one barrier to
+//                    turn the per-wave counts into bases -- and scatters them.
+//                    Every workgroup repeats the small scan instead of one
+//                    workgroup doing it in a launch of its own in between.
+// The same code groups tokens by their expert set (TOK = true, k a template
+// parameter so that a token's k ids load together) for the expert-set down
+// projection. The pair grouping and the token grouping share the launches,
+// each workgroup serving one of the two jobs.
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
 
 namespace cm {
 
 constexpr int kGroupThreads = 256;
-constexpr int kScanStageMax = 8192;  // block counts staged in LDS by the scan (32 KB)
 
-// Token t's expert set: its k ids with ids >= E replaced by E, sorted
+
+// Token t's expert set: its K ids with ids >= E replaced by E, sorted
 // ascending (stable in j); the key reads them as base-(E+1) digits, most
 // significant first. rank[j] is slot j's position in that order.
-__device__ __forceinline__ int token_set_key(const uint32_t* __restrict__ idx, long long t, int k, int E,
-                                             int (&rank)[kSetMaxK]) {
-    int ex[kSetMaxK];
-    for (int j = 0; j < k; ++j) {
-        const uint32_t v = idx[t * k + j];
-        ex[j] = v < (uint32_t)E ? (int)v : E;
-    }
+template <int K>
+__device__ __forceinline__ int token_set_key_of(const uint32_t (&raw)[K], int E, int (&rank)[K]) {
+    int ex[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) ex[j] = raw[j] < (uint32_t)E ? (int)raw[j] : E;
     int key = 0;
-    for (int j = 0; j < k; ++j) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
         int r = 0;
-        for (int i = 0; i < k; ++i) r += (ex[i] < ex[j]) || (ex[i] == ex[j] && i < j);
+#pragma unroll
+        for (int i = 0; i < K; ++i) r += (ex[i] < ex[j]) || (ex[i] == ex[j] && i < j);
         rank[j] = r;
     }
     // digits in sorted order: position r holds the slot with rank r
-    for (int r = 0; r < k; ++r) {
+#pragma unroll
+    for (int r = 0; r < K; ++r) {
         int d = E;
-        for (int j = 0; j < k; ++j) d = (rank[j] == r) ? ex[j] : d;
+#pragma unroll
+        for (int j = 0; j < K; ++j) d = (rank[j] == r) ? ex[j] : d;
         key = key * (E + 1) + d;
     }
     return key;
 }
 
-// Bin of item i: the expert of pair i (TOK = false, -1 if dropped), or the
-// expert-set key of token i (TOK = true).
-template <bool TOK>
-__device__ __forceinline__ int item_bin(const uint32_t* __restrict__ idx, long long i, int k, int E,
-                                        int (&rank)[kSetMaxK]) {
+// The expert ids of item i (TOK: the K ids of token i; else pair i's id),
+// loaded apart from their use so that a caller can have other loads in
+// flight before it waits for these.
+template <bool TOK, int K>
+__device__ __forceinline__ void item_load(const uint32_t* __restrict__ idx, long long i, uint32_t (&raw)[K]) {
     if constexpr (TOK) {
-        return token_set_key(idx, i, k, E, rank);
+#pragma unroll
+        for (int j = 0; j < K; ++j) raw[j] = idx[i * K + j];
     } else {
-        const uint32_t e = __builtin_nontemporal_load(idx + i);
-        return e < (uint32_t)E ? (int)e : -1;
+        raw[0] = __builtin_nontemporal_load(idx + i);
     }
+}
+// Bin of an item from its ids: the expert of a pair (-1 if dropped), or the
+// expert-set key of a token.
+template <bool TOK, int K>
+__device__ __forceinline__ int item_bin_of(const uint32_t (&raw)[K], int E, int (&rank)[K]) {
+    if constexpr (TOK) {
+        return token_set_key_of<K>(raw, E, rank);
+    } else {
+        return raw[0] < (uint32_t)E ? (int)raw[0] : -1;
+    }
+}
+template <bool TOK, int K>
+__device__ __forceinline__ int item_bin(const uint32_t* __restrict__ idx, long long i, int E, int (&rank)[K]) {
+    uint32_t raw[K];
+    item_load<TOK, K>(idx, i, raw);
+    return item_bin_of<TOK, K>(raw, E, rank);
 }
 
 // Histogram of block blk of job j into s_cnt ([4 waves][nbins] of LDS).
-template <bool TOK>
+template <bool TOK, int K>
 __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
     const uint32_t* __restrict__ idx = j.idx;
     const long long P = j.items;
-    const int k = j.k, E = j.E, nbins = j.nbins;
+    const int E = j.E, nbins = j.nbins;
     int32_t* __restrict__ block_counts = j.b.block_counts;
     const int wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
-    __syncthreads();
     constexpr int IPT = kGroupChunk / kGroupThreads;  // items per thread
     const long long base = (long long)blk * kGroupChunk;
     int32_t* mine = s_cnt + wave * nbins;
-    int rank[kSetMaxK];
+    int rank[K];
     // the bins of all IPT items first, so that their loads are in flight
-    // together, then the LDS counts
+    // together (and under the LDS clear), then the LDS counts
     int bin[IPT];
 #pragma unroll
     for (int s = 0; s < IPT; ++s) {
         const long long p = base + s * kGroupThreads + threadIdx.x;
-        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        bin[s] = p < P ? item_bin<TOK, K>(idx, p, E, rank) : -1;
     }
+    for (int i = threadIdx.x; i < 4 * nbins; i += kGroupThreads) s_cnt[i] = 0;
+    __syncthreads();
 #pragma unroll
     for (int s = 0; s < IPT; ++s)
         if (bin[s] >= 0) atomicAdd(mine + bin[s], 1);
@@ -102,22 +123,32 @@ __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
 }
 
 // Exclusive scans of u[0..n) and v[0..n) in place (one workgroup of
-// kGroupThreads), returning the totals; s_part is 8 ints of scratch. Each
+// kGroupThreads), returning the totals and the largest u; s_part is 12 ints
+// of scratch. Each
 // thread scans a contiguous run of ceil(n / threads) entries of both; the
 // per-thread sums are scanned inside each wave by shuffles and across the 4
 // waves through LDS (two barriers).
 __device__ void block_exclusive_scan2(int32_t* u, int32_t* v, int n, int32_t* s_part, int32_t& total_u,
-                                      int32_t& total_v) {
+                                      int32_t& total_v, int32_t& max_u) {
     constexpr int NW = kGroupThreads / 64;
     const int per = (n + kGroupThreads - 1) / kGroupThreads;
     const int lo = threadIdx.x * per;
     const int hi = lo + per < n ? lo + per : n;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int32_t ru = 0, rv = 0;
+    int32_t ru = 0, rv = 0, mu = 0;
     for (int i = lo; i < hi; ++i) {
         ru += u[i];
         rv += v[i];
+        mu = u[i] > mu ? u[i] : mu;
     }
+    // largest u: wave butterfly, then the wave maxima through LDS (one
+    // same-address LDS atomic per lane serialises at full latency)
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t t = __shfl_xor(mu, d);
+        mu = t > mu ? t : mu;
+    }
+    if (lane == 0) s_part[2 * NW + wave] = mu;
     int32_t iu = ru, iv = rv;  // inclusive within the wave
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -135,15 +166,17 @@ __device__ void block_exclusive_scan2(int32_t* u, int32_t* v, int n, int32_t* s_
     int32_t bu = iu - ru, bv = iv - rv;
     total_u = 0;
     total_v = 0;
+    max_u = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        const int32_t wu = s_part[w], wv = s_part[NW + w];
+        const int32_t wu = s_part[w], wv = s_part[NW + w], wm = s_part[2 * NW + w];
         if (w < wave) {
             bu += wu;
             bv += wv;
         }
         total_u += wu;
         total_v += wv;
+        max_u = wm > max_u ? wm : max_u;
     }
     for (int i = lo; i < hi; ++i) {
         const int32_t cu = u[i], cv = v[i];
@@ -155,131 +188,90 @@ __device__ void block_exclusive_scan2(int32_t* u, int32_t* v, int n, int32_t* s_
     __syncthreads();
 }
 
-// One workgroup. block_counts[b][e] becomes the number of bin-e items in
-// blocks < b (its base inside the bin's segment): bins go round-robin to the
-// waves, each scans its bin over the blocks 64 at a time. Then the bin totals
-// and tile counts are scanned into offsets and the tile table. Also clears
-// zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs).
-__device__ void scan_body(const GroupJob& j, int32_t* s_tot) {
-    // LDS: [nbins] totals -> offsets, [nbins] tile counts -> bases, [threads],
-    // then (when it fits) the [nblocks][nbins] block counts, staged so that each
-    // bin is scanned by one thread from LDS; otherwise bins go round-robin to
-    // the waves, which scan them from global memory 64 blocks at a time
-    const int nblocks = j.nb, nbins = j.nbins, BM = j.BM;
-    int32_t* __restrict__ block_counts = j.b.block_counts;
-    int32_t* __restrict__ offsets = j.b.offsets;
-    int32_t* __restrict__ tile_row = j.b.tile_row;
-    int32_t* __restrict__ tile_exp = j.b.tile_exp;
-    int32_t* __restrict__ num_tiles = j.b.num_tiles;
-    int32_t* __restrict__ zero_ptr = j.b.zero_ptr;
-    const int zero_n = j.b.zero_n;
-    int32_t* s_tb = s_tot + nbins;
-    int32_t* s_part = s_tb + nbins;
-    __shared__ int32_t s_max;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int ncounts = nblocks * nbins;
-    const bool staged = ncounts <= kScanStageMax;
-    int32_t* s_bc = s_part + kGroupThreads;
-    if (threadIdx.x == 0) s_max = 0;
-    for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
-    if (staged) {
-        for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) s_bc[i] = block_counts[i];
-        __syncthreads();
-    }
-    // Few bins over many blocks (the pair grouping): each wave scans whole
-    // bins, its lanes over the blocks 64 at a time. Otherwise (the token-set
-    // grouping: many bins, fewer blocks) one thread per bin walks its column
-    // of the staged counts (the LDS reads are independent, only the running
-    // sum is serial).
-    const bool by_wave = !staged || ((nbins + kGroupThreads / 64 - 1) / (kGroupThreads / 64)) * 2 < nblocks;
-    if (staged && !by_wave) {
-        for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
-            int32_t run = 0;
-            for (int b = 0; b < nblocks; ++b) {
-                const int32_t c = s_bc[b * nbins + e];
-                s_bc[b * nbins + e] = run;
-                run += c;
-            }
-            s_tot[e] = run;
-            s_tb[e] = (run + BM - 1) / BM;
-        }
-    }
-    int32_t* bc = staged ? s_bc : block_counts;
-    for (int e = wave; e < (by_wave ? nbins : 0); e += kGroupThreads / 64) {
-        int32_t carry = 0;
-        for (int b0 = 0; b0 < nblocks; b0 += 64) {
-            const int b = b0 + lane;
-            const long long o = (long long)b * nbins + e;
-            const int32_t c = b < nblocks ? bc[o] : 0;
-            int32_t incl = c;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int32_t t = __shfl_up(incl, d);
-                if (lane >= d) incl += t;
-            }
-            if (b < nblocks) bc[o] = carry + incl - c;
-            carry += __shfl(incl, 63);
-        }
-        if (lane == 0) {
-            s_tot[e] = carry;
-            s_tb[e] = (carry + BM - 1) / BM;
-        }
-    }
-    __syncthreads();
-    if (staged)
-        for (int i = threadIdx.x; i < ncounts; i += kGroupThreads) block_counts[i] = s_bc[i];
-    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) atomicMax(&s_max, s_tot[e]);
-    int32_t total, tiles;
-    block_exclusive_scan2(s_tot, s_tb, nbins, s_part, total, tiles);
-    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
-        offsets[e] = s_tot[e];
-        const int32_t c = (e + 1 < nbins ? s_tot[e + 1] : total) - s_tot[e];
-        const int32_t nt = (c + BM - 1) / BM;
-        for (int i = 0; i < nt; ++i) {
-            tile_row[s_tb[e] + i] = s_tot[e] + i * BM;
-            tile_exp[s_tb[e] + i] = e;
-        }
-    }
-    if (threadIdx.x == 0) {
-        offsets[nbins] = total;
-        offsets[nbins + 1] = s_max;
-        *num_tiles = tiles;
-    }
-}
-
-// Stable scatter of one kGroupChunk block. Wave w ranks items
-// [w*64*IPT, (w+1)*64*IPT) of the block, 64 at a time: lanes holding the same
-// bin find each other with ballots over the bin's bits, and a per-wave LDS
-// count per bin carries the rank from one step to the next. After one barrier
-// the per-wave counts become per-wave bases (block base of the bin + counts
-// of the waves before), and every item goes to base + its rank.
-template <bool TOK>
-__device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
+// Stable scatter of one kGroupChunk block, with the scan of the block counts
+// done by every workgroup for itself. The counts of all blocks (the previous
+// launch's output) give, per bin, the total over all blocks and the base over
+// the blocks before this one. Wave w ranks items [w*64*IPT, (w+1)*64*IPT) of
+// the block, 64 at a time: lanes holding the same bin find each other with
+// ballots over the bin's bits, and a per-wave LDS count per bin carries the
+// rank from one step to the next. One block-wide scan of the totals gives the
+// bin offsets (workgroup 0 also stores offsets, tile table, tile count, the
+// largest bin, and clears zero_n ints at zero_ptr).
+// After one more barrier the per-wave counts become per-wave positions and
+// every item goes to position + its rank.
+// LDS: [NW][nbins] per-wave counts, [nbins] totals, [nbins] tile counts,
+// [nbins] bases, [threads] scan scratch.
+template <bool TOK, int K>
+__device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem) {
     constexpr int NW = kGroupThreads / 64;
     constexpr int IPT = kGroupChunk / kGroupThreads;  // items per lane
-    // LDS s_wc: [NW][nbins] per-wave counts, then bases
     const uint32_t* __restrict__ idx = j.idx;
     const long long P = j.items;
-    const int k = j.k, E = j.E, nbins = j.nbins, ebits = j.ebits;
+    const int E = j.E, nbins = j.nbins, ebits = j.ebits, BM = j.BM, nblocks = j.nb;
     const int32_t* __restrict__ block_counts = j.b.block_counts;
-    const int32_t* __restrict__ offsets = j.b.offsets;
     int32_t* __restrict__ sorted_pair = j.b.sorted_pair;
     int32_t* __restrict__ pair_dest = j.pair_dest;
+    int32_t* s_wc = s_mem;
+    int32_t* s_tot = s_wc + NW * nbins;
+    int32_t* s_tb = s_tot + nbins;
+    int32_t* s_base = s_tb + nbins;
+    int32_t* s_part = s_base + nbins;
+    const int ncounts = nblocks * nbins;  // < 2^31 (checked by the launcher)
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_wc[i] = 0;
-    __syncthreads();
-    int32_t* mine = s_wc + wave * nbins;
     const long long wbase = (long long)blk * kGroupChunk + wave * 64 * IPT;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int bin[IPT], lrank[IPT];
-    int rank[kSetMaxK];
-    // the bins first, so that the loads of all IPT items are in flight together
+    int rank[IPT][K];  // slot ranks of each token in its expert set (TOK)
+    // Global loads first, all in flight together: this block's items, then
+    // the first round of the count table. Bin totals over all blocks and bases
+    // over the blocks before this one are summed by groups of G lanes per bin
+    // (G a power of two, G * nbins <= threads): lane j of bin e's group adds
+    // blocks j, j + G, ... in registers, a butterfly over the group's lanes
+    // sums the G parts (no LDS atomics: same-address ones serialise).
+    uint32_t raw[IPT][K];
 #pragma unroll
     for (int s = 0; s < IPT; ++s) {
         const long long p = wbase + s * 64 + lane;
-        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        if (p < P) item_load<TOK, K>(idx, p, raw[s]);
     }
+    int G = 1;
+    while (G < 64 && 2 * G * nbins <= kGroupThreads) G *= 2;
+    const int gj = (int)threadIdx.x & (G - 1), ge = (int)threadIdx.x / G, estep = kGroupThreads / G;
+    constexpr int U = 16;
+    for (int e0 = 0; e0 < nbins; e0 += estep) {
+        const int e = e0 + ge;
+        int32_t tot = 0, bas = 0;
+        for (int b0 = gj; b0 < nblocks; b0 += U * G) {
+            int32_t c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int b2 = b0 + u * G;
+                c[u] = (e < nbins && b2 < nblocks) ? block_counts[b2 * nbins + e] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                tot += c[u];
+                bas += (b0 + u * G < blk) ? c[u] : 0;
+            }
+        }
+        for (int m = 1; m < G; m <<= 1) {
+            tot += __shfl_xor(tot, m);
+            bas += __shfl_xor(bas, m);
+        }
+        if (e < nbins && gj == 0) {
+            s_tot[e] = tot;
+            s_base[e] = bas;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < IPT; ++s) {
+        const long long p = wbase + s * 64 + lane;
+        bin[s] = p < P ? item_bin_of<TOK, K>(raw[s], E, rank[s]) : -1;
+    }
+    for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_wc[i] = 0;
+    __syncthreads();
+    int32_t* mine = s_wc + wave * nbins;
 #pragma unroll
     for (int s = 0; s < IPT; ++s) {
         const int b = bin[s];
@@ -298,9 +290,33 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
         if (active && r == 0) mine[b] = before + __popcll(peers);
         lrank[s] = before + r;
     }
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) s_tb[e] = (s_tot[e] + BM - 1) / BM;
     __syncthreads();
+    int32_t total, tiles, largest;
+    block_exclusive_scan2(s_tot, s_tb, nbins, s_part, total, tiles, largest);  // s_tot -> offsets
+    if (blk == 0) {
+        int32_t* __restrict__ offsets = j.b.offsets;
+        int32_t* __restrict__ tile_row = j.b.tile_row;
+        int32_t* __restrict__ tile_exp = j.b.tile_exp;
+        for (int i = threadIdx.x; i < j.b.zero_n; i += kGroupThreads) j.b.zero_ptr[i] = 0;
+        for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+            offsets[e] = s_tot[e];
+            const int32_t c = (e + 1 < nbins ? s_tot[e + 1] : total) - s_tot[e];
+            const int32_t nt = (c + BM - 1) / BM;
+            for (int i = 0; i < nt; ++i) {
+                tile_row[s_tb[e] + i] = s_tot[e] + i * BM;
+                tile_exp[s_tb[e] + i] = e;
+            }
+        }
+        if (threadIdx.x == 0) {
+            offsets[nbins] = total;
+            offsets[nbins + 1] = largest;
+            *j.b.num_tiles = tiles;
+        }
+    }
+    // per-wave positions: bin offset + blocks before + waves before
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
-        int32_t run = offsets[e] + block_counts[(long long)blk * nbins + e];
+        int32_t run = s_tot[e] + s_base[e];
         for (int w = 0; w < NW; ++w) {
             const int32_t c = s_wc[w * nbins + e];
             s_wc[w * nbins + e] = run;
@@ -315,8 +331,8 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
         const int32_t pos = mine[bin[s]] + lrank[s];
         sorted_pair[pos] = (int32_t)p;
         if constexpr (TOK) {
-            (void)token_set_key(idx, p, k, E, rank);
-            for (int j = 0; j < k; ++j) pair_dest[p * k + j] = pos * k + rank[j];
+#pragma unroll
+            for (int jj = 0; jj < K; ++jj) pair_dest[p * K + jj] = pos * K + rank[s][jj];
         }
     }
 }
@@ -329,12 +345,12 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_wc) {
 // table, and then per-wave bases, so each item goes to base + its rank. Also
 // clears zero_n ints at zero_ptr (the split-K arrival counters of the GEMMs
 // that follow).
-template <bool TOK>
+template <bool TOK, int K>
 __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
     constexpr int NW = kGroupThreads / 64;
     constexpr int IPT = kGroupSmallMax / kGroupThreads;  // items per lane
     const uint32_t* __restrict__ idx = j.idx;
-    const int P = (int)j.items, k = j.k, E = j.E, nbins = j.nbins, ebits = j.ebits, BM = j.BM;
+    const int P = (int)j.items, E = j.E, nbins = j.nbins, ebits = j.ebits, BM = j.BM;
     int32_t* __restrict__ offsets = j.b.offsets;
     int32_t* __restrict__ sorted_pair = j.b.sorted_pair;
     int32_t* __restrict__ tile_row = j.b.tile_row;
@@ -347,20 +363,18 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
     int32_t* s_off = s_mem + NW * nbins;  // [nbins] bin totals -> offsets
     int32_t* s_tb = s_off + nbins;        // [nbins] tile counts -> tile bases
     int32_t* s_part = s_tb + nbins;       // scan scratch
-    __shared__ int32_t s_max;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wbase = wave * 64 * IPT;
     int bin[IPT], lrank[IPT];
-    int rank[kSetMaxK];
+    int rank[IPT][K];  // slot ranks of each token in its expert set (TOK)
     // the bins first: the loads of all IPT items are in flight together
 #pragma unroll
     for (int s = 0; s < IPT; ++s) {
         const int p = wbase + s * 64 + lane;
-        bin[s] = p < P ? item_bin<TOK>(idx, p, k, E, rank) : -1;
+        bin[s] = p < P ? item_bin<TOK, K>(idx, p, E, rank[s]) : -1;
     }
     for (int i = threadIdx.x; i < zero_n; i += kGroupThreads) zero_ptr[i] = 0;
     for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_cnt[i] = 0;
-    if (threadIdx.x == 0) s_max = 0;
     __syncthreads();
     int32_t* mine = s_cnt + wave * nbins;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -389,11 +403,10 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
         for (int w = 0; w < NW; ++w) c += s_cnt[w * nbins + e];
         s_off[e] = c;
         s_tb[e] = (c + BM - 1) / BM;
-        atomicMax(&s_max, c);
     }
     __syncthreads();
-    int32_t total, tiles;
-    block_exclusive_scan2(s_off, s_tb, nbins, s_part, total, tiles);
+    int32_t total, tiles, largest;
+    block_exclusive_scan2(s_off, s_tb, nbins, s_part, total, tiles, largest);
     for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
         offsets[e] = s_off[e];
         const int32_t c = (e + 1 < nbins ? s_off[e + 1] : total) - s_off[e];
@@ -412,7 +425,7 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
     }
     if (threadIdx.x == 0) {
         offsets[nbins] = total;
-        offsets[nbins + 1] = s_max;
+        offsets[nbins + 1] = largest;
         *num_tiles = tiles;
     }
     __syncthreads();
@@ -423,37 +436,35 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
         const int32_t pos = mine[bin[s]] + lrank[s];
         sorted_pair[pos] = p;
         if constexpr (TOK) {
-            (void)token_set_key(idx, p, k, E, rank);
-            for (int jj = 0; jj < k; ++jj) pair_dest[(long long)p * k + jj] = pos * k + rank[jj];
+#pragma unroll
+            for (int jj = 0; jj < K; ++jj) pair_dest[(long long)p * K + jj] = pos * K + rank[s][jj];
         }
     }
 }
 
-// The three launches serve the pair grouping (A) and, on the expert-set path,
-// the token grouping (B) together: workgroups [0, A.nb) work on A and the rest
-// on B; in the middle launch workgroup 0 is A's scan (or its whole grouping if
-// A is small) and workgroup 1 the same for B.
+// The launches serve the pair grouping (A) and, on the expert-set path, the
+// token grouping (B, KB ids per token) together: in each, the first
+// workgroups work on A and the rest on B. A job of at most kGroupSmallMax
+// items is done whole by one workgroup of the final launch; a larger one
+// takes a workgroup per kGroupChunk items in both launches.
+template <int KB>
 __global__ __launch_bounds__(kGroupThreads) void grouping_hist_k(GroupJob A, GroupJob B) {
     extern __shared__ int32_t s_dyn[];
     const int a_nb = A.small ? 0 : A.nb;
-    if ((int)blockIdx.x < a_nb) hist_body<false>(A, blockIdx.x, s_dyn);
-    else hist_body<true>(B, blockIdx.x - a_nb, s_dyn);
+    if ((int)blockIdx.x < a_nb) hist_body<false, 1>(A, blockIdx.x, s_dyn);
+    else if constexpr (KB > 0) hist_body<true, KB>(B, blockIdx.x - a_nb, s_dyn);
 }
-__global__ __launch_bounds__(kGroupThreads) void grouping_mid_k(GroupJob A, GroupJob B, int has_b) {
+template <int KB>
+__global__ __launch_bounds__(kGroupThreads) void grouping_final_k(GroupJob A, GroupJob B) {
     extern __shared__ int32_t s_dyn[];
-    if (blockIdx.x == 0) {
-        if (A.small) small_body<false>(A, s_dyn);
-        else scan_body(A, s_dyn);
-    } else if (has_b) {
-        if (B.small) small_body<true>(B, s_dyn);
-        else scan_body(B, s_dyn);
+    const int a_n = A.small ? 1 : A.nb;
+    if ((int)blockIdx.x < a_n) {
+        if (A.small) small_body<false, 1>(A, s_dyn);
+        else scatter_body<false, 1>(A, blockIdx.x, s_dyn);
+    } else if constexpr (KB > 0) {
+        if (B.small) small_body<true, KB>(B, s_dyn);
+        else scatter_body<true, KB>(B, blockIdx.x - a_n, s_dyn);
     }
-}
-__global__ __launch_bounds__(kGroupThreads) void grouping_scatter_k(GroupJob A, GroupJob B) {
-    extern __shared__ int32_t s_dyn[];
-    const int a_nb = A.small ? 0 : A.nb;
-    if ((int)blockIdx.x < a_nb) scatter_body<false>(A, blockIdx.x, s_dyn);
-    else scatter_body<true>(B, blockIdx.x - a_nb, s_dyn);
 }
 
 static GroupJob make_job(const uint32_t* idx, long long items, int k, int E, int nbins, int BM,
@@ -484,28 +495,43 @@ GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, i
     return make_job(idx, T, k, E, nkeys, BM, b, pair_dest);
 }
 
+template <int KB>
+static hipError_t launch_groupings_k(const GroupJob& A, const GroupJob& B, bool has_b, hipStream_t stream) {
+    auto ints = [](long long n) { return (size_t)n * sizeof(int32_t); };
+    const bool a_multi = !A.small, b_multi = has_b && !B.small;
+    const int nb_multi = (a_multi ? A.nb : 0) + (b_multi ? B.nb : 0);
+    if (nb_multi > 0) {
+        const int bins = std::max(a_multi ? A.nbins : 0, b_multi ? B.nbins : 0);
+        hipLaunchKernelGGL(grouping_hist_k<KB>, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins), stream, A, B);
+    }
+    auto final_lds = [&](const GroupJob& j) {
+        return j.small ? 6LL * j.nbins + kGroupThreads : 7LL * j.nbins + kGroupThreads;
+    };
+    const long long lds = std::max(final_lds(A), has_b ? final_lds(B) : 0LL);
+    const int grid = (A.small ? 1 : A.nb) + (has_b ? (B.small ? 1 : B.nb) : 0);
+    hipLaunchKernelGGL(grouping_final_k<KB>, dim3(grid), dim3(kGroupThreads), ints(lds), stream, A, B);
+    return hipGetLastError();
+}
+
 hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t stream) {
     if (B && (B->k < 1 || B->k > kSetMaxK || B->nbins > kSetMaxKeys)) return hipErrorInvalidValue;
-    GroupJob b = B ? *B : GroupJob{};
-    if (!B) b.small = true;  // nothing of B in the multi-workgroup launches
-    const int nb_multi = (A.small ? 0 : A.nb) + (b.small ? 0 : b.nb);
-    auto ints = [](long long n) { return (size_t)n * sizeof(int32_t); };
-    const int bins_multi = std::max(A.small ? 0 : A.nbins, b.small ? 0 : b.nbins);
-    if (nb_multi > 0) {
-        hipLaunchKernelGGL(grouping_hist_k, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins_multi), stream, A, b);
+    // the scatter workgroups index the per-block count table with 32-bit ints
+    if ((long long)A.nb * A.nbins + 16LL * kGroupThreads >= 0x7fffffffLL ||
+        (B && (long long)B->nb * B->nbins + 16LL * kGroupThreads >= 0x7fffffffLL))
+        return hipErrorInvalidValue;
+    const GroupJob b = B ? *B : GroupJob{};
+    switch (B ? B->k : 0) {
+        case 0: return launch_groupings_k<0>(A, b, false, stream);
+        case 1: return launch_groupings_k<1>(A, b, true, stream);
+        case 2: return launch_groupings_k<2>(A, b, true, stream);
+        case 3: return launch_groupings_k<3>(A, b, true, stream);
+        case 4: return launch_groupings_k<4>(A, b, true, stream);
+        case 5: return launch_groupings_k<5>(A, b, true, stream);
+        case 6: return launch_groupings_k<6>(A, b, true, stream);
+        case 7: return launch_groupings_k<7>(A, b, true, stream);
+        case 8: return launch_groupings_k<8>(A, b, true, stream);
+        default: return hipErrorInvalidValue;
     }
-    auto mid_lds = [&](const GroupJob& j) {
-        const long long counts = (long long)j.nb * j.nbins;
-        return j.small ? 6LL * j.nbins + kGroupThreads
-                       : 2LL * j.nbins + kGroupThreads + (counts <= kScanStageMax ? counts : 0);
-    };
-    const long long mid = std::max(mid_lds(A), B ? mid_lds(*B) : 0LL);
-    hipLaunchKernelGGL(grouping_mid_k, dim3(B ? 2 : 1), dim3(kGroupThreads), ints(mid), stream, A, b, B ? 1 : 0);
-    if (nb_multi > 0) {
-        hipLaunchKernelGGL(grouping_scatter_k, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins_multi), stream, A,
-                           b);
-    }
-    return hipGetLastError();
 }
 
 }  // namespace cm
