@@ -62,6 +62,8 @@ def parse():
                     help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
     ap.add_argument("--no-router-shapes", dest="router_shapes", action="store_false",
                     help="skip the topk-softmax config-2 shapes reported next to the MoE step")
+    ap.add_argument("--no-fp8-decode", dest="fp8_decode", action="store_false",
+                    help="skip the decode GEMM timings with bf16 against fp8 expert weights")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the warmup, run 3 plain copy kernels of MIB MiB (read MIB, write MIB; "
                          "the reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -201,6 +203,7 @@ def main():
     # fused_moe symbol adding into it, ffi.rs:35), timed the same way
     dropin = bench_dropin(torch, L, x, gate, up, down, topk_w, topk_i, wl, act, args)
     router = bench_router_shapes(torch, cm, dev, args) if args.router_shapes else None
+    fp8 = bench_fp8_decode(torch, cm, dev, args) if args.fp8_decode else None
 
     c = 6 if qwen3 else 4
     flops = float(T) * k * c * H * I
@@ -246,6 +249,7 @@ def main():
         "graph_ms_per_step": round(graph_ms, 4) if graph_ms else None,
         "dropin_fused_moe": dropin,
         "topk_softmax_config2": router,
+        "fp8_decode": fp8,
         "kernels_note": "HIP-event averages per launch: gemm_gate_up from the timed steps (the only kernel "
                         "bracketed there), the others from an untimed pass of up to 10 steps with every "
                         "launch bracketed",
@@ -401,6 +405,80 @@ def bench_router_shapes(torch, cm, dev, args):
                      "gbs": round(nbytes / (gus * 1e-6) / 1e9, 1) if gus else None,
                      "hbm_frac": round(nbytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4) if gus else None}
         del logits
+    return res
+
+
+def bench_fp8_decode(torch, cm, dev, args):
+    """Decode GEMMs with bf16 against fp8 e4m3 expert weights
+    (candle_moe_fused_moe_status against candle_moe_fused_moe_fp8, the same
+    inputs and routing): µs per launch of the gate/up and down GEMMs from HIP
+    events around every launch, over 60 calls rotating across weight copies
+    whose total exceeds the 256 MB last-level cache twice (cold weights),
+    and the weight bytes each GEMM streams (touched experts x 2HI or HI x bytes
+    per weight) over its time."""
+    L = cm.lib()
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nslots = L.candle_moe_profile_begin()
+    cm.check(L.candle_moe_profile_end(None, None, 0))
+    names = [L.candle_moe_profile_slot_name(s).decode() for s in range(nslots)]
+    res = {}
+    for wname, T in [("qwen3", 16), ("qwen3", 64), ("q30b", 1), ("q30b", 16)]:
+        wl = WORKLOADS[wname]
+        H, I, E, k = wl["H"], wl["I"], wl["E"], wl["k"]
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + T)
+        ncopy = max(2, -(-(1024 << 20) // (3 * E * H * I)))  # fp8 bytes of all copies >= 1 GiB
+        x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.randn((T, E), generator=g, device=dev)
+        if wl["zipf"]:
+            ranks = torch.randperm(E, generator=torch.Generator().manual_seed(args.seed)).double() + 1
+            pz = ranks ** (-wl["zipf"])
+            logits += torch.log(pz / pz.sum()).float().to(dev)[None, :]
+        tw = torch.empty((T, k), device=dev)
+        ti = torch.empty((T, k), dtype=torch.int32, device=dev)
+        tei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        cm.apply_topk_softmax_inplace(logits, tw, ti, tei)
+        touched = int(torch.unique(ti).numel())
+        bf, f8 = [], []
+        for _ in range(ncopy):
+            w3 = [(torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+                  for shape in ((E, H, I), (E, H, I), (E, I, H))]
+            bf.append(w3)
+            f8.append([cm.quantize_fp8(w, input_kn=True) for w in w3])
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+        def run(fp8, c):
+            if fp8:
+                (gq, gs), (uq, us_), (dq, ds) = f8[c]
+                return L.candle_moe_fused_moe_fp8(p(x), p(gq), p(uq), p(dq), p(gs), p(us_), p(ds), p(tw), p(ti),
+                                                  p(out), T, H, I, E, k, 0, 0, 1, stream)
+            gw, uw, dw = bf[c]
+            return L.candle_moe_fused_moe_status(p(x), p(gw), p(uw), p(dw), p(tw), p(ti), p(out), T, H, I, E, k, 0,
+                                                 0, 1, stream)
+
+        entry = {"tokens": T, "touched_experts": touched, "weight_copies": ncopy}
+        for label, fp8 in (("bf16", False), ("fp8", True)):
+            for c in range(ncopy):
+                cm.check(run(fp8, c))
+            torch.cuda.synchronize()
+            L.candle_moe_profile_begin()
+            for s in range(60):
+                cm.check(run(fp8, s % ncopy))
+            torch.cuda.synchronize()
+            ms = (ctypes.c_double * nslots)()
+            cnt = (ctypes.c_int * nslots)()
+            cm.check(L.candle_moe_profile_end(ms, cnt, nslots))
+            us = {names[s]: round(1000.0 * ms[s] / cnt[s], 2) for s in range(nslots) if cnt[s]}
+            bpe = 1 if fp8 else 2
+            g1b, g2b = touched * 2 * H * I * bpe, touched * H * I * bpe
+            us["gate_up_gbs"] = round(g1b / (us["gemm_gate_up"] * 1e-6) / 1e9, 1)
+            us["down_gbs"] = round(g2b / (us["gemm_down"] * 1e-6) / 1e9, 1)
+            entry[label] = us
+        b, f = entry["bf16"], entry["fp8"]
+        entry["gemm_speedup"] = round((b["gemm_gate_up"] + b["gemm_down"]) / (f["gemm_gate_up"] + f["gemm_down"]), 3)
+        res[f"{wname}_T{T}"] = entry
+        del bf, f8
     return res
 
 

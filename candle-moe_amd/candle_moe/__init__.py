@@ -106,6 +106,12 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_noalloc.restype = i32
         L.candle_moe_fused_moe_noalloc_scratch_bytes.argtypes = []
         L.candle_moe_fused_moe_noalloc_scratch_bytes.restype = sz
+        L.candle_moe_quantize_fp8.argtypes = [vp, u32, i32, i32, i32, i32, vp, vp, vp]
+        L.candle_moe_quantize_fp8.restype = i32
+        L.candle_moe_dequantize_fp8.argtypes = [vp, vp, i32, i32, i32, vp, u32, vp]
+        L.candle_moe_dequantize_fp8.restype = i32
+        L.candle_moe_fused_moe_fp8.argtypes = [vp] * 4 + [vp] * 3 + [vp] * 3 + [i32] * 6 + [u32, u32, vp]
+        L.candle_moe_fused_moe_fp8.restype = i32
         L.candle_moe_set_combine_policy.argtypes = [i32]
         L.candle_moe_set_combine_policy.restype = i32
         L.candle_moe_set_tile_policy.argtypes = [i32]
@@ -282,6 +288,59 @@ def router_topk(hidden, router_weight, topk_weight, topk_indices, token_expert_i
         _stream_for(hidden)))
 
 
+def quantize_fp8(weights, input_kn: bool = True):
+    """FP8 e4m3 codes and per-output-channel f32 scales of expert weights
+    (candle_moe_quantize_fp8). weights [E, K, N] (input_kn, the reference's
+    gate/up/fc1 layout) or [E, N, K] (down/fc2, already [E, H, I]), f32/f16/bf16,
+    contiguous, on the GPU -> (codes [E, N, K] uint8, scales [E, N] f32) with
+    weights[e, k, n] ~ decode(codes[e, n, k]) * scales[e, n]."""
+    import torch
+
+    if not weights.is_contiguous() or weights.dim() != 3:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "quantize_fp8: weights must be contiguous [E, K, N] or [E, N, K]")
+    E = weights.shape[0]
+    K, N = (weights.shape[1], weights.shape[2]) if input_kn else (weights.shape[2], weights.shape[1])
+    codes = torch.empty((E, N, K), dtype=torch.uint8, device=weights.device)
+    scales = torch.empty((E, N), dtype=torch.float32, device=weights.device)
+    check(lib().candle_moe_quantize_fp8(ctypes.c_void_p(weights.data_ptr()), _torch_dtype_code(weights), E, K, N,
+                                        1 if input_kn else 0, ctypes.c_void_p(codes.data_ptr()),
+                                        ctypes.c_void_p(scales.data_ptr()), _stream_for(weights)))
+    return codes, scales
+
+
+def dequantize_fp8(codes, scales, dtype):
+    """decode(codes) * scales as [E, N, K] of torch dtype (candle_moe_dequantize_fp8)."""
+    import torch
+
+    E, N, K = codes.shape
+    if tuple(scales.shape) != (E, N) or scales.dtype != torch.float32 or not codes.is_contiguous() \
+            or not scales.is_contiguous():
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "dequantize_fp8: codes [E, N, K] u8 and scales [E, N] f32")
+    out = torch.empty((E, N, K), dtype=dtype, device=codes.device)
+    check(lib().candle_moe_dequantize_fp8(ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
+                                          E, N, K, ctypes.c_void_p(out.data_ptr()), _torch_dtype_code(out),
+                                          _stream_for(codes)))
+    return out
+
+
+def fused_moe_fp8(input, gate_q, up_q, down_q, gate_scale, up_scale, down_scale, routing_weights, expert_indices,
+                  output, num_experts: int, top_k: int, activation: int = 0, moe_type: int = 0) -> None:
+    """output += MoE of input over fp8 expert weights (candle_moe_fused_moe_fp8).
+    Qwen3 (moe_type 0): gate_q/up_q [E, I, H] u8 with scales [E, I], down_q
+    [E, H, I] with down_scale [E, H]. Nomic (moe_type 1, fc1 / fc2 in gate /
+    up as for fused_moe): gate_q = fc1 [E, I, H] with gate_scale [E, I], up_q =
+    fc2 [E, H, I] with up_scale [E, H] (down_q and down_scale None).
+    input/output [T, H] f16 or bf16; routing_weights
+    [T, k] f32; expert_indices [T, k] u32/i32."""
+    T, H = input.shape
+    I = gate_q.shape[1]
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    check(lib().candle_moe_fused_moe_fp8(
+        p(input), p(gate_q), p(up_q), p(down_q), p(gate_scale), p(up_scale), p(down_scale), p(routing_weights),
+        p(expert_indices), p(output), T, H, I, num_experts, top_k, activation, moe_type,
+        _torch_dtype_code(input), _stream_for(input)))
+
+
 def validate_topk_softmax(g: CmTensor, w: CmTensor, i: CmTensor, ei: CmTensor) -> None:
     check(lib().candle_moe_validate_topk_softmax(ctypes.byref(g), ctypes.byref(w), ctypes.byref(i), ctypes.byref(ei)))
 
@@ -399,5 +458,5 @@ def fused_moe_tile(num_tokens, hidden_dim, intermediate_dim, num_experts, top_k,
 __all__ = [
     "Activation", "FusedMoE", "apply_topk_softmax_inplace", "CandleMoeError", "lib", "describe", "spec",
     "validate_topk_softmax", "version", "LIB_PATH", "set_combine_policy", "fused_moe_path",
-    "set_tile_policy", "fused_moe_tile", "fused_moe_kernel",
+    "set_tile_policy", "fused_moe_tile", "fused_moe_kernel", "quantize_fp8", "dequantize_fp8", "fused_moe_fp8",
 ]

@@ -244,8 +244,10 @@ static Layout make_layout(const Problem& p) {
 // runs). out16: so does the output (the expert-set down GEMM stores straight
 // into it, 8 bytes at a time; otherwise the pair path, whose last pass
 // handles any alignment).
+// fp8: fp8 weights (candle_moe_fused_moe_fp8): the 32-row kernel for every
+// batch, on the pair path.
 static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
-                         Problem& p, bool aligned16 = true, bool out16 = true) {
+                         Problem& p, bool aligned16 = true, bool out16 = true, bool fp8 = false) {
     if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
     if (H < 1 || I < 1)
         return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: hidden_dim and intermediate_dim must be >= 1 (got %d, %d)", H, I);
@@ -290,7 +292,13 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     } else if (!p.mfma || is_f32_cfg(p.cfg)) {
         p.cfg = kTileSimt;
     }
-    if (p.mfma && !g_tile_policy) {
+    if (fp8) {
+        if (p.dtype == kF32 || H % 16 || I % 16 || !p.mfma)
+            return set_error(CANDLE_MOE_ERR_UNSUPPORTED,
+                             "fused_moe_fp8: needs f16 or bf16 activations, hidden_dim and intermediate_dim multiples "
+                             "of 16 and 16-byte aligned tensors (got dtype %u, %d, %d)", dtype, H, I);
+        p.cfg = kLdsRows32;
+    } else if (p.mfma && !g_tile_policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
@@ -301,7 +309,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     if (is_lds_cfg(p.cfg)) {
         const long long es = 2;
         const long long lim = 0x7fffff00LL;
-        if ((long long)T * H * es >= lim || P * I * es >= lim || (long long)H * I * es >= lim) p.cfg = kTile128;
+        if ((long long)T * H * es >= lim || P * I * es >= lim || (long long)H * I * es >= lim) {
+            if (fp8) return set_error(CANDLE_MOE_ERR_UNSUPPORTED, "fused_moe_fp8: operands beyond 2 GiB");
+            p.cfg = kTile128;
+        }
     }
     p.BM = tile_rows(p.cfg);
     // Expert-set path: each distinct sorted expert set becomes one GEMM group
@@ -313,7 +324,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // 404 us at T=12288).
     p.set_path = false;
     p.nkeys = 0;
-    if (p.mfma && out16 && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
+    if (p.mfma && !fp8 && out16 && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
         long long nk = 1;
         for (int j = 0; j < k && nk <= kSetMaxKeys; ++j) nk *= (E + 1);
         if (nk <= kSetMaxKeys) {
@@ -391,8 +402,19 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     return CANDLE_MOE_OK;
 }
 
+// fp8 expert weights of candle_moe_fused_moe_fp8 (codes [E][N][K], scales [E][N])
+struct Fp8Weights {
+    const float* gate_scale;
+    const float* up_scale;
+    const float* down_scale;
+};
+
 static int run_moe(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
-                   const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, hipStream_t s) {
+                   const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, hipStream_t s,
+                   const Fp8Weights* f8 = nullptr) {
+    auto gemm = [&](int mode, const GemmArgs& g) {
+        return f8 ? launch_moe_gemm_w8(mode, p.dtype, g, s) : launch_moe_gemm(mode, p.dtype, p.cfg, g, s);
+    };
     const Layout L = make_layout(p);
     GroupingBufs gb = {};
     gb.offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
@@ -473,9 +495,14 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.fold_w = p.set_path ? 1 : 0;
     g1.n_experts = p.E;
     g1.seg_len = p.I;
+    if (f8) {  // codes [E][I][H]: n-rows of H bytes
+        g1.ldb = p.H;
+        g1.scale0 = f8->gate_scale;
+        g1.scale1 = f8->up_scale;
+    }
     {
         ProfScope ps(kSlotGemm1, s);
-        e = launch_moe_gemm(mode1, p.dtype, p.cfg, g1, s);
+        e = gemm(mode1, g1);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe gate/up GEMM");
 
@@ -537,9 +564,14 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.counters = counters;
     g2.zero_f32 = nullptr;
     g2.zero_n = 0;
+    if (f8) {  // codes [E][H][I] (down, or Nomic's fc2 in up): n-rows of I bytes
+        g2.ldb = p.I;
+        g2.scale0 = qwen3 ? f8->down_scale : f8->up_scale;
+        g2.scale1 = nullptr;
+    }
     {
         ProfScope ps(kSlotGemm2, s);
-        e = launch_moe_gemm(mode2, p.dtype, p.cfg, g2, s);
+        e = gemm(mode2, g2);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM");
 
@@ -623,12 +655,13 @@ int trim_owned_workspaces() {
 
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
-                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream) {
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream,
+                   const Fp8Weights* f8) {
     clear_error();
     Problem p;
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const bool aligned16 = a16(x) && a16(gate) && a16(up) && a16(down);
-    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out));
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out), f8 != nullptr);
     if (rc) return rc;
     rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
     if (rc) return rc;
@@ -642,7 +675,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
         if ((uintptr_t)ws % 256)
             return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: workspace must be 256-byte aligned");
         return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw),
-                       reinterpret_cast<const uint32_t*>(idx), out, overwrite, reinterpret_cast<char*>(ws), s);
+                       reinterpret_cast<const uint32_t*>(idx), out, overwrite, reinterpret_cast<char*>(ws), s, f8);
     }
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -652,7 +685,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
     if (!w) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s", L.total,
                              hipGetErrorString(e));
     return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                   out, overwrite, reinterpret_cast<char*>(w->ptr), s);
+                   out, overwrite, reinterpret_cast<char*>(w->ptr), s, f8);
 }
 
 // ----------------------------------------------- fused MoE without allocation
@@ -797,6 +830,50 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
     return cm::fused_moe_impl(input, gate_weights, up_weights, down_weights, routing_weights, expert_indices, output,
                               num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
                               activation_type, moe_type, dtype, workspace, workspace_bytes, false, false, stream);
+}
+
+int candle_moe_fused_moe_fp8(const void* input, const void* gate_q, const void* up_q, const void* down_q,
+                             const float* gate_scale, const float* up_scale, const float* down_scale,
+                             const void* routing_weights, const void* expert_indices, void* output, int num_tokens,
+                             int hidden_dim, int intermediate_dim, int num_experts, int num_selected_experts,
+                             int activation_type, uint32_t moe_type, uint32_t dtype, void* stream) {
+    cm::clear_error();
+    if (num_tokens > 0) {
+        if (!gate_scale || (moe_type == 0 && (!up_scale || !down_scale)) || (moe_type == 1 && !up_scale))
+            return cm::set_error(CANDLE_MOE_ERR_INVALID, "fused_moe_fp8: null scale pointer");
+        if (!up_q) return cm::set_error(CANDLE_MOE_ERR_INVALID, "fused_moe_fp8: null tensor pointer");
+    }
+    const cm::Fp8Weights f8 = {gate_scale, up_scale, down_scale};
+    return cm::fused_moe_impl(input, gate_q, up_q, down_q, routing_weights, expert_indices, output, num_tokens,
+                              hidden_dim, intermediate_dim, num_experts, num_selected_experts, activation_type,
+                              moe_type, dtype, nullptr, 0, true, false, stream, &f8);
+}
+
+int candle_moe_quantize_fp8(const void* weights, uint32_t dtype, int num_experts, int k_dim, int n_dim, int input_kn,
+                            void* codes, float* scales, void* stream) {
+    cm::clear_error();
+    if (dtype > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "quantize_fp8: dtype must be 0, 1 or 2 (got %u)", dtype);
+    if (num_experts < 0 || k_dim < 0 || n_dim < 0)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "quantize_fp8: sizes must be >= 0");
+    if ((long long)num_experts * k_dim * n_dim == 0) return CANDLE_MOE_OK;
+    if (!weights || !codes || !scales) return cm::set_error(CANDLE_MOE_ERR_INVALID, "quantize_fp8: null pointer");
+    const hipError_t e = cm::launch_quantize_fp8(weights, (int)dtype, num_experts, k_dim, n_dim, input_kn ? 1 : 0,
+                                                 reinterpret_cast<uint8_t*>(codes), scales,
+                                                 reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "quantize_fp8 launch");
+}
+
+int candle_moe_dequantize_fp8(const void* codes, const float* scales, int num_experts, int n_dim, int k_dim, void* out,
+                              uint32_t dtype, void* stream) {
+    cm::clear_error();
+    if (dtype > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "dequantize_fp8: dtype must be 0, 1 or 2 (got %u)", dtype);
+    if (num_experts < 0 || k_dim < 0 || n_dim < 0)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "dequantize_fp8: sizes must be >= 0");
+    if ((long long)num_experts * k_dim * n_dim == 0) return CANDLE_MOE_OK;
+    if (!codes || !scales || !out) return cm::set_error(CANDLE_MOE_ERR_INVALID, "dequantize_fp8: null pointer");
+    const hipError_t e = cm::launch_dequantize_fp8(reinterpret_cast<const uint8_t*>(codes), scales, num_experts, n_dim,
+                                                   k_dim, out, (int)dtype, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "dequantize_fp8 launch");
 }
 
 // Scratch of candle_moe_group_pairs: per-block counts and the row-tile table

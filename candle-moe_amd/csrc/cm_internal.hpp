@@ -111,6 +111,10 @@ struct GemmArgs {
     // round's workgroups fill the XCD's CUs; the splits meet in the fixup
     // through partial [8*tail_cus][BM*BN] f32 and counters [8*tail_cus].
     int tail_cus;
+    // fp8 weights (launch_moe_gemm_w8): per-output-column f32 scales, [E][N],
+    // of B0 and (kGateUp) B1
+    const float* scale0;
+    const float* scale1;
 };
 constexpr int kTailMaxSplit = 8;
 constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter splits lose to the fixup)
@@ -170,8 +174,21 @@ bool mfma_supported(int dtype, int K, int N);
 int gemm_tile_cols(int mode, int cfg);
 hipError_t launch_moe_gemm(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
+// GEMMs over OCP fp8 e4m3 weights stored K-contiguous ([E][N][K] bytes, ldb
+// = K, strideB = N*K) with per-output-column scales (scale0 / scale1), on the
+// 32-row kernel (tile_rows(kLdsRows32)); 16-bit activations; modes kGateUp,
+// kFc1, kDown, kFc2.
+hipError_t launch_moe_gemm_w8(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
+
+// fp8 weight preparation (fp8.hip): quantize [E][K][N] (kn) or [E][N][K]
+// weights of dtype to e4m3 codes [E][N][K] and scales [E][N]; dequantize
+// codes and scales to [E][N][K] of dtype.
+hipError_t launch_quantize_fp8(const void* w, int dtype, int E, int K, int N, int kn, uint8_t* q, float* scales,
+                               hipStream_t stream);
+hipError_t launch_dequantize_fp8(const uint8_t* q, const float* scales, int E, int N, int K, void* out, int dtype,
+                                 hipStream_t stream);
 
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);
@@ -190,8 +207,10 @@ int set_error(int code, const char* fmt, ...);
 void clear_error();
 int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void* ei, int E, int T, int k,
                       void* stream);
+struct Fp8Weights;
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
-                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream);
+                   uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream,
+                   const Fp8Weights* f8 = nullptr);
 
 }  // namespace cm

@@ -114,6 +114,24 @@ __device__ __forceinline__ u32x4 tr_pair(const char* p_lo, const char* p_hi) {
     return v;
 }
 
+// Eight OCP fp8 e4m3 values (bytes of v, lowest first) as the MFMA operand of
+// the activation dtype: v_cvt_pk_f32_fp8 decodes two bytes to f32 (every
+// e4m3 value is exact in bf16 and f16, so the packing conversion is exact).
+template <int DT>
+__device__ __forceinline__ u32x4 fp8x8_to(const u32x2& v) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], true);
+    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], false);
+    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], true);
+    u32x4 r;
+    r[0] = pack2<DT>(a[0], a[1]);
+    r[1] = pack2<DT>(b[0], b[1]);
+    r[2] = pack2<DT>(c[0], c[1]);
+    r[3] = pack2<DT>(d[0], d[1]);
+    return r;
+}
+
 // Split-K fixup. Every split writes its f32 partial tile to partial slot
 // slot0 + ks (per wave, per 32x32 block, 4 registers of a lane as one 16-byte
 // chunk, lanes contiguous), then counts itself in a.counters[ctr]; the split
@@ -250,16 +268,25 @@ __device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int
 //                   (each output row is owned by one tile)
 //  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
 //  kDownRows / kFc2Rows: rows[p] = dtype(w * acc)      (the pair's own row)
+// sc0 / sc1 (fp8 weights, else null): per-output-column scales of the
+// tile's expert (gate / up for kGateUp), applied to the f32 sums first.
 template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
                                               int wm, int wn, int lane, const int32_t* s_tok, const float* s_w,
-                                              const int* pre_dst = nullptr, const float* pre_w = nullptr) {
+                                              const int* pre_dst = nullptr, const float* pre_w = nullptr,
+                                              const float* sc0 = nullptr, const float* sc1 = nullptr) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
     const int N = a.N;
     const int lr = lane & 31, lh = lane >> 5;
     if constexpr (ATOMIC) {
         float* C = reinterpret_cast<float*>(a.C);
+        float cs[NB];  // this lane's column scale per block
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int col = nt * BN + wn * WN + nb * 32 + lr;
+            cs[nb] = (sc0 && col < N) ? sc0[col] : 1.0f;
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
@@ -271,7 +298,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     const int col = nt * BN + wn * WN + nb * 32 + lr;
-                    if (col < N) unsafeAtomicAdd(C + rowoff + col, w * acc[mb][nb][i]);
+                    if (col < N) unsafeAtomicAdd(C + rowoff + col, w * (cs[nb] * acc[mb][nb][i]));
                 }
             }
         }
@@ -308,10 +335,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
                             float h[4];
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
+                                // (fp8 weights: the column scales first)
+                                const float s0 = sc0 ? sc0[col + j] : 1.0f;
                                 if constexpr (DUAL) {
-                                    h[j] = act_t<ACT>(acc[mb][2 * q][4 * g + j]) * acc[mb][2 * q + 1][4 * g + j];
+                                    const float s1 = sc1 ? sc1[col + j] : 1.0f;
+                                    h[j] = act_t<ACT>(s0 * acc[mb][2 * q][4 * g + j]) * (s1 * acc[mb][2 * q + 1][4 * g + j]);
                                 } else {
-                                    h[j] = act_t<ACT>(acc[mb][q][4 * g + j]);
+                                    h[j] = act_t<ACT>(s0 * acc[mb][q][4 * g + j]);
                                 }
                                 h[j] *= wscale;
                             }

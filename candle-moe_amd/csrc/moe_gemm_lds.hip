@@ -29,7 +29,7 @@ namespace cm {
 
 using namespace lds;
 
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, int WGM = 2, int OCC = 1>
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, int WGM = 2, int OCC = 1, bool W8 = false>
 __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // NW waves in WGM rows: 4 in a 2x2 layout (one per SIMD), 8 in 2x4 (two
     // per SIMD, so one wave's MFMAs cover the other's LDS, DMA and VALU work),
@@ -53,7 +53,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     constexpr int RPA = 1024 / AROW;       // K-contiguous rows per DMA instruction
     constexpr int KSTEPS = BK / 16;
     constexpr int A_BYTES = BM * AROW;
-    constexpr int B_BYTES = BN * AROW;
+    // W8: fp8 e4m3 weights, K-contiguous ([N,K] per expert, one byte per
+    // element), each n-row of a B sub-tile BK bytes of KCH 16-byte chunks
+    constexpr int KROW = BK;
+    constexpr int KCH = KROW / 16;
+    constexpr int KRPI = 1024 / KROW;  // fp8 n-rows per DMA instruction
+    constexpr int B_BYTES = W8 ? BN * KROW : BN * AROW;
     constexpr int STAGE = A_BYTES + B_BYTES;
     constexpr int A_INS = A_BYTES / (1024 * NW);  // DMA instructions per wave per stage
     constexpr int B_INS = B_BYTES / (1024 * NW);
@@ -70,7 +75,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     static_assert(A_INS * 1024 * NW == A_BYTES && SUB_INS * 1024 * NW == SUB_BYTES, "DMA split");
     static_assert(!DUAL || (WN % 64) == 0, "gate/up pairs must stay inside one wave");
     static_assert(BNK || BCH >= 8, "[K,N] tiles need >= 8 chunks per row for the swizzle");
-    static_assert(BNK || SUB_INS * NSUB == B_INS, "B tile split");
+    static_assert(BNK || W8 || SUB_INS * NSUB == B_INS, "B tile split");
+    constexpr int W8_SUB_BYTES = SUBN * KROW;
+    constexpr int W8_SUB_INS = W8_SUB_BYTES / (1024 * NW);
+    static_assert(!W8 || (!BNK && KCH == 4 && W8_SUB_INS * 1024 * NW == W8_SUB_BYTES && W8_SUB_INS * NSUB == B_INS),
+                  "fp8 B tile");
     static_assert(LOADS * (NST - 2) < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
     __shared__ int32_t s_tok[(ATOMIC || SET) ? BM : 1];
@@ -139,7 +148,15 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     uint32_t b_off[B_INS];
 #pragma unroll
     for (int i = 0; i < B_INS; ++i) {
-        if constexpr (BNK) {
+        if constexpr (W8) {
+            // n-row r of sub-tile i / W8_SUB_INS; the lane's slot receives the
+            // chunk a_swz(r, slot) of that row (byte offsets: one byte per k)
+            const int q = NW * (i % W8_SUB_INS) + wave;
+            const int r = KRPI * q + lane / KCH;
+            const int n = nt * SUBN + r;
+            const int kc = a_swz<KCH>(r, lane % KCH) * 16;
+            b_off[i] = n < N ? (uint32_t)n * (uint32_t)a.ldb + (uint32_t)kc : kOob;
+        } else if constexpr (BNK) {
             const int r = RPA * (NW * i + wave) + lane / ACH;
             const int n = nt * BN + r;
             const int kc = a_swz<ACH>(r, lane % ACH) * 8;
@@ -158,10 +175,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // calls come in increasing k0).
     int seg = 0, seg_k0 = 0;
     auto weights_rsrc = [&](int e, i32x4& r0s, i32x4& r1s) {
-        const long long eoff = (long long)e * a.strideB;
-        r0s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B0) + eoff, a.strideB * 2);
+        constexpr int BES = W8 ? 1 : 2;  // bytes per weight element
+        const long long eoff = (long long)e * a.strideB * BES;
+        r0s = make_rsrc(reinterpret_cast<const char*>(a.B0) + eoff, a.strideB * BES);
         r1s = r0s;
-        if constexpr (DUAL) r1s = make_rsrc(reinterpret_cast<const uint16_t*>(a.B1) + eoff, a.strideB * 2);
+        if constexpr (DUAL) r1s = make_rsrc(reinterpret_cast<const char*>(a.B1) + eoff, a.strideB * BES);
     };
     i32x4 rB0, rB1;
     weights_rsrc(seg_exp[0], rB0, rB1);
@@ -186,7 +204,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         // a tile that lies inside the operands in K takes the SGPR-offset path;
         // a K tail checks every lane's chunk against K
         const uint32_t sa = (uint32_t)k0 * 2u;
-        const uint32_t sb = BNK ? (uint32_t)kk * 2u : (uint32_t)kk * (uint32_t)a.ldb * 2u;
+        const uint32_t sb = W8 ? (uint32_t)kk : (BNK ? (uint32_t)kk * 2u : (uint32_t)kk * (uint32_t)a.ldb * 2u);
         if (k0 + BK <= K && kk + BK <= klim) {
             // the tile lies inside the operands in K: one SGPR offset for all lanes
 #pragma unroll
@@ -195,7 +213,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < B_INS; ++i) {
                 if (A_INS + i < lo || A_INS + i >= hi) continue;
-                if constexpr (BNK) {
+                if constexpr (W8) {
+                    const int sub = i / W8_SUB_INS;
+                    dma16s(sub ? rB1 : rB0, sB + sub * W8_SUB_BYTES + (NW * (i % W8_SUB_INS) + wave) * 1024, b_off[i],
+                           sb);
+                } else if constexpr (BNK) {
                     dma16s(rB0, sB + (NW * i + wave) * 1024, b_off[i], sb);
                 } else {
                     const int sub = i / SUB_INS;  // compile-time after unrolling
@@ -214,7 +236,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < B_INS; ++i) {
                 if (A_INS + i < lo || A_INS + i >= hi) continue;
-                if constexpr (BNK) {
+                if constexpr (W8) {
+                    // (K is a multiple of 16: a chunk lies wholly inside or outside)
+                    const int sub = i / W8_SUB_INS;
+                    const int r = KRPI * (NW * (i % W8_SUB_INS) + wave) + lane / KCH;
+                    const bool in = kk + a_swz<KCH>(r, lane % KCH) * 16 < klim;
+                    dma16s(sub ? rB1 : rB0, sB + sub * W8_SUB_BYTES + (NW * (i % W8_SUB_INS) + wave) * 1024,
+                           in ? b_off[i] : kOob, sb);
+                } else if constexpr (BNK) {
                     const int r = RPA * (NW * i + wave) + lane / ACH;
                     const bool in = kk + a_swz<ACH>(r, lane % ACH) * 8 < klim;
                     dma16s(rB0, sB + (NW * i + wave) * 1024, in ? b_off[i] : kOob, sb);
@@ -264,7 +293,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            if constexpr (BNK) {
+            if constexpr (W8) {
+                // 8 fp8 weights (k = 16 kk + 8 lh .. +7 of n-row r), converted
+                // exactly to the activation dtype
+                const int sub = DUAL ? (nb & 1) : 0;
+                const int r = DUAL ? wn * (WN / 2) + (nb >> 1) * 32 + lr : wn * WN + nb * 32 + lr;
+                const char* q8 = sB + sub * W8_SUB_BYTES + r * KROW + a_swz<KCH>(r, kk) * 16 + lh * 8;
+                bfr[nb] = fp8x8_to<DT>(*reinterpret_cast<const u32x2*>(q8));
+            } else if constexpr (BNK) {
                 const int r = wn * WN + nb * 32 + lr;
                 bfr[nb] = *reinterpret_cast<const u32x4*>(sB + r * AROW + a_swz<ACH>(r, c) * 16);
             } else {
@@ -287,7 +323,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     };
     // LDS read instructions per k16 step (ds_read_b128 for A and [N,K] B,
     // two ds_read_b64_tr_b16 per [K,N] B block).
-    constexpr int DS_PER_STEP = MB + (BNK ? NB : 2 * NB);
+    constexpr int DS_PER_STEP = MB + ((BNK || W8) ? NB : 2 * NB);
     constexpr int MFMA_PER_STEP = MB * NB;
     // Pin the schedule of one region: one MFMA, then one LDS read, while
     // reads remain, then the remaining MFMAs (masks: 0x8 MFMA, 0x100 DS read).
@@ -502,9 +538,16 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         if (nsplit > 1 && !splitk_fixup<MB, NB, NW, FIX_BATCH>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
             return;
     }
+    // fp8 weights: per-output-channel scales of this tile's expert
+    const float* sc0 = nullptr;
+    const float* sc1 = nullptr;
+    if constexpr (W8) {
+        sc0 = a.scale0 + (long long)grp * N;
+        if constexpr (DUAL) sc1 = a.scale1 + (long long)grp * N;
+    }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
                                                 (GATHER || ROWS) ? pre_dst : nullptr,
-                                                (GATHER || ROWS) ? pre_w : nullptr);
+                                                (GATHER || ROWS) ? pre_w : nullptr, sc0, sc1);
 }
 
 template <int DT, int MODE>
@@ -541,6 +584,33 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
         }
     }
     return hipGetLastError();
+}
+
+// fp8-weight GEMMs: the 32-row kernel (decode), pair-path modes only
+template <int DT, int MODE>
+static hipError_t launch_w8_mode(const GemmArgs& a, hipStream_t stream) {
+    const long long tiles = (long long)a.m_tiles_max * a.n_tiles;
+    const long long nwg_l = split_grid(tiles, a);
+    if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (nwg_l <= 0) return hipSuccess;
+    hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1, 1, true>), dim3((int)nwg_l), dim3(256), 0, stream,
+                       a);
+    return hipGetLastError();
+}
+template <int DT>
+static hipError_t launch_w8_dt(int mode, const GemmArgs& a, hipStream_t stream) {
+    switch (mode) {
+        case kGateUp: return launch_w8_mode<DT, kGateUp>(a, stream);
+        case kFc1: return launch_w8_mode<DT, kFc1>(a, stream);
+        case kDown: return launch_w8_mode<DT, kDown>(a, stream);
+        case kFc2: return launch_w8_mode<DT, kDown>(a, stream);  // [N,K] fp8 weights: the same kernel
+        default: return hipErrorInvalidValue;
+    }
+}
+hipError_t launch_moe_gemm_w8(int mode, int dtype, const GemmArgs& a, hipStream_t stream) {
+    if (dtype == kBF16) return launch_w8_dt<kBF16>(mode, a, stream);
+    if (dtype == kF16) return launch_w8_dt<kF16>(mode, a, stream);
+    return hipErrorInvalidValue;
 }
 
 template <int DT>

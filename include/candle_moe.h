@@ -211,6 +211,39 @@ size_t candle_moe_grouping_workspace_size(int num_pairs, int num_experts);
 int candle_moe_group_pairs(const void* expert_indices, int num_pairs, int num_experts, void* offsets,
                            void* sorted_pairs, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Opt-in FP8 expert weights (no counterpart in the reference, whose fused_moe
+ * takes the weights in the activation dtype, /root/reference/src/lib.rs:273-335;
+ * for decode, where the weight stream is the whole cost). Format: OCP FP8
+ * e4m3 (E4M3FN: bias 7, largest finite 448, no infinities, 0x7F/0xFF NaN),
+ * one f32 scale per output channel, codes K-contiguous:
+ *   codes [E][N][K] u8, scales [E][N] f32, w[e][k][n] ~ decode(codes[e][n][k]) * scales[e][n]
+ *   scale = max_k |w[e][k][n]| / 448 (1 for an all-zero channel),
+ *   code = e4m3(w / scale), round to nearest even, |x| >= 448 -> +-448.
+ * quantize_fp8: weights [E][K][N] (input_kn = 1: gate/up [E][H][I] and
+ * down [E][I][H] of Qwen3, fc1 [E][H][I] of Nomic, the reference's layouts)
+ * or [E][N][K] (input_kn = 0: fc2 of Nomic, [E][H][I]) in dtype 0/1/2. */
+int candle_moe_quantize_fp8(const void* weights, uint32_t dtype, int num_experts, int k_dim, int n_dim,
+                            int input_kn, void* codes, float* scales, void* stream);
+/* out [E][N][K] of dtype = dtype(decode(codes) * scales): the weights the fp8
+ * MoE multiplies by. */
+int candle_moe_dequantize_fp8(const void* codes, const float* scales, int num_experts, int n_dim, int k_dim,
+                              void* out, uint32_t dtype, void* stream);
+/* fused_moe with fp8 expert weights: output += the MoE of input over the
+ * dequantized weights, f32 accumulation (as candle_moe_fused_moe_status,
+ * accumulating). Qwen3 (moe_type 0): gate_q/up_q codes [E][I][H] with scales
+ * [E][I] (quantize_fp8 of gate/up [E][H][I]), down_q [E][H][I] with scales
+ * [E][H] (of down [E][I][H]). Nomic (moe_type 1), as fused_moe takes fc1 /
+ * fc2 in gate / up: gate_q = fc1 codes [E][I][H] with gate_scale [E][I],
+ * up_q = fc2 codes [E][H][I] with up_scale [E][H]; down_q and down_scale
+ * unused. Activations f16 or bf16;
+ * hidden_dim and intermediate_dim multiples of 16; every tensor 16-byte
+ * aligned. Runs the 32-row GEMM kernel at every batch size. */
+int candle_moe_fused_moe_fp8(const void* input, const void* gate_q, const void* up_q, const void* down_q,
+                             const float* gate_scale, const float* up_scale, const float* down_scale,
+                             const void* routing_weights, const void* expert_indices, void* output, int num_tokens,
+                             int hidden_dim, int intermediate_dim, int num_experts, int num_selected_experts,
+                             int activation_type, uint32_t moe_type, uint32_t dtype, void* stream);
+
 /* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status
  * and the FusedMoE forward (hipFreeAsync on the stream each was used on); the
  * next call allocates again. No counterpart in the reference, whose fused_moe

@@ -52,6 +52,12 @@ def lib():
         L.om_preprocess.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp]
         L.om_fused_moe.argtypes = [vp] * 8 + [i32] * 9 + [vp, i32, i32]
         L.om_fused_moe.restype = i32
+        L.om_e4m3_decode.argtypes = [ctypes.c_uint8]
+        L.om_e4m3_decode.restype = f32
+        L.om_e4m3_encode.argtypes = [f32]
+        L.om_e4m3_encode.restype = ctypes.c_uint8
+        L.om_quantize_fp8.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
+        L.om_dequantize_fp8.argtypes = [vp, vp, ctypes.c_size_t, i32, vp]
         _lib = L
     return _lib
 
@@ -168,4 +174,37 @@ def fused_moe(x, gate, up, down, w, idx, *, E: int, k: int, act: int, moe_type: 
                             T, H, I, E, k, act, moe_type, dtype, mode, _p(r), nr, nthreads)
     if rc != 0:
         raise ValueError(f"om_fused_moe rejected its arguments (code {rc})")
+    return out
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """Exact f32 values of e4m3 codes (NaN for 0x7F / 0xFF)."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    return np.array([lib().om_e4m3_decode(int(v)) for v in c.ravel()], np.float32).reshape(c.shape)
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """Nearest e4m3 codes of f32 values (ties to even, saturating at 448)."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    return np.array([lib().om_e4m3_encode(float(v)) for v in a.ravel()], np.uint8).reshape(a.shape)
+
+
+def quantize_fp8(w: np.ndarray, dtype: int, kn: bool = True):
+    """FP8 weight format: w [E,K,N] (kn) or [E,N,K] storage of dtype ->
+    (codes [E,N,K] u8, scales [E,N] f32)."""
+    w = np.ascontiguousarray(w)
+    E = w.shape[0]
+    K, N = (w.shape[1], w.shape[2]) if kn else (w.shape[2], w.shape[1])
+    q = np.empty((E, N, K), np.uint8)
+    s = np.empty((E, N), np.float32)
+    lib().om_quantize_fp8(_p(w), dtype, E, K, N, 1 if kn else 0, _p(q), _p(s))
+    return q, s
+
+
+def dequantize_fp8(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """decode(q) * s as f32 [E,N,K]."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    out = np.empty(q.shape, np.float32)
+    lib().om_dequantize_fp8(_p(q), _p(s), s.size, q.shape[-1], _p(out))
     return out

@@ -434,3 +434,77 @@ int om_fused_moe(const void* x, const void* gate, const void* up, const void* do
     free(omap);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* FP8 expert weights: OCP 8-bit floating point e4m3 (E4M3FN of the    */
+/* OCP OFP8 specification, v1.0): 1 sign, 4 exponent (bias 7) and 3    */
+/* mantissa bits, no infinities, S.1111.111 is NaN, largest finite 448. */
+/* The product format (candle_moe_quantize_fp8) adds one f32 scale per  */
+/* output channel; it has no counterpart in the reference.             */
+/* ------------------------------------------------------------------ */
+float om_e4m3_decode(uint8_t c) {
+    const int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);             /* subnormal: m/8 * 2^(1-7) */
+    else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);   /* normal: (1 + m/8) * 2^(e-7) */
+    return s ? -v : v;
+}
+
+/* Nearest e4m3 value, ties to the even code (round to nearest even); |x| at
+ * or above 448 saturates to +-448, NaN gives 0x7F; the sign of a zero result
+ * is kept. Written as a search over the 127 finite magnitudes (monotone in
+ * the code), not by bit manipulation. */
+static uint8_t e4m3_encode_tab(float x, const double* mag) {
+    if (isnan(x)) return 0x7f;
+    const uint8_t sign = signbit(x) ? 0x80 : 0x00;
+    const double a = fabs((double)x);
+    if (a >= 448.0) return sign | 0x7e;
+    int lo = 0, hi = 0x7e; /* largest code with value <= a */
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (mag[mid] <= a) lo = mid; else hi = mid - 1;
+    }
+    const double d0 = a - mag[lo], d1 = mag[lo + 1] - a; /* exact in f64 */
+    int c = lo;
+    if (d1 < d0 || (d1 == d0 && (lo & 1))) c = lo + 1;
+    return sign | (uint8_t)c;
+}
+
+static void e4m3_magnitudes(double mag[128]) {
+    for (int c = 0; c < 128; ++c) mag[c] = c < 0x7f ? (double)om_e4m3_decode((uint8_t)c) : INFINITY;
+}
+
+uint8_t om_e4m3_encode(float x) {
+    double mag[128];
+    e4m3_magnitudes(mag);
+    return e4m3_encode_tab(x, mag);
+}
+
+void om_quantize_fp8(const void* w, int dtype, int E, int K, int N, int kn, uint8_t* q, float* scales) {
+    double mag[128];
+    e4m3_magnitudes(mag);
+    const size_t slab = (size_t)K * N;
+    float* ws = (float*)malloc(sizeof(float) * (slab > 0 ? slab : 1));
+    for (int e = 0; e < E; ++e) {
+        load_row(w, (size_t)e * slab, (int)slab, dtype, ws); /* the expert's weights as f32 */
+#pragma omp parallel for schedule(static)
+        for (int n = 0; n < N; ++n) {
+            float amax = 0.0f;
+            for (int k = 0; k < K; ++k) amax = fmaxf(amax, fabsf(ws[kn ? (size_t)k * N + n : (size_t)n * K + k]));
+            const float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
+            scales[(size_t)e * N + n] = sc;
+            uint8_t* Q = q + ((size_t)e * N + n) * K;
+            for (int k = 0; k < K; ++k) Q[k] = e4m3_encode_tab(ws[kn ? (size_t)k * N + n : (size_t)n * K + k] / sc, mag);
+        }
+    }
+    free(ws);
+}
+
+void om_dequantize_fp8(const uint8_t* q, const float* scales, size_t rows, int K, float* out) {
+    float dec[256];
+    for (int c = 0; c < 256; ++c) dec[c] = om_e4m3_decode((uint8_t)c);
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; ++r)
+        for (int k = 0; k < K; ++k) out[r * K + k] = dec[q[r * K + k]] * scales[r];
+}

@@ -21,6 +21,12 @@
  *   om_topk_softmax    float64 softmax + stable argsort (numpy), closed-form
  *                      special cases (E=1, equal logits, k=E), planted ties
  *   om_preprocess      brute-force counting sort + invariants
+ *   om_e4m3_decode     all 256 codes against the OCP e4m3 formula evaluated
+ *                      independently and against torch.float8_e4m3fn
+ *   om_e4m3_encode     torch.float8_e4m3fn rounding on every finite value, every
+ *                      midpoint and its f32 neighbours, subnormals; saturation
+ *   om_quantize_fp8    the channel maximum encodes to +-448, layout symmetry
+ *                      (kn vs the transposed nk input), zero channels
  *   om_fused_moe       float64 dense matmul (numpy) per expert, one-hot routing
  *                      == dense MLP, k=1/w=1 exact expert MLP, linearity in w
  * Per-op dtype rounding of candle's f16/bf16 path (activation op sequence,
@@ -104,6 +110,21 @@ int om_fused_moe(const void* x, const void* gate, const void* up, const void* do
                  double* out, int T, int H, int I, int E, int k, int act,
                  int moe_type, int dtype, int mode, const int32_t* rows,
                  int n_rows, int nthreads);
+
+/*
+ * FP8 expert weights (the product's opt-in format, no counterpart in the
+ * reference). OCP OFP8 e4m3 (E4M3FN): bias 7, no infinities, 0x7F/0xFF NaN.
+ * decode: exact value of a code. encode: nearest value, ties to the even
+ * code, |x| >= 448 -> +-448, NaN -> 0x7F.
+ * quantize: w [E][K][N] (kn = 1) or [E][N][K] (kn = 0) of dtype ->
+ *   scales[e][n] = max_k |w| / 448 (f32 division; 1 for a zero channel),
+ *   q[e][n][k] = encode(w / scales[e][n]) (f32 division).
+ * dequantize: out[r][k] = decode(q[r][k]) * scales[r] (one f32 product).
+ */
+float om_e4m3_decode(uint8_t c);
+uint8_t om_e4m3_encode(float x);
+void om_quantize_fp8(const void* w, int dtype, int E, int K, int N, int kn, uint8_t* q, float* scales);
+void om_dequantize_fp8(const uint8_t* q, const float* scales, size_t rows, int K, float* out);
 
 #ifdef __cplusplus
 }

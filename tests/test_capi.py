@@ -294,3 +294,29 @@ def test_noalloc_rejects_without_launch():
                                           None) == cm.CANDLE_MOE_ERR_INVALID
     assert L.candle_moe_fused_moe_noalloc(None, None, None, None, None, None, None, 0, 64, 256, 8, 2, 0, 0, 1,
                                           None) == cm.CANDLE_MOE_OK
+
+
+def test_fp8_entry_points_reject_without_launch():
+    L = cm.lib()
+    p = ctypes.c_void_p(256)
+    # f32 activations, and hidden/intermediate sizes off the 16-element grid
+    rc = L.candle_moe_fused_moe_fp8(p, p, p, p, p, p, p, p, p, p, 16, 64, 256, 8, 2, 0, 0, 2, None)
+    assert rc == cm.CANDLE_MOE_ERR_UNSUPPORTED and "fused_moe_fp8" in cm.last_error()
+    rc = L.candle_moe_fused_moe_fp8(p, p, p, p, p, p, p, p, p, p, 16, 72, 256, 8, 2, 0, 0, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_UNSUPPORTED
+    rc = L.candle_moe_fused_moe_fp8(p, p, p, p, p, p, p, p, p, p, 16, 64, 200, 8, 2, 0, 0, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_UNSUPPORTED
+    # missing scales (Qwen3 needs all three, Nomic gate and up)
+    rc = L.candle_moe_fused_moe_fp8(p, p, p, p, p, p, None, p, p, p, 16, 64, 256, 8, 2, 0, 0, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_INVALID and "scale" in cm.last_error()
+    rc = L.candle_moe_fused_moe_fp8(p, p, p, None, p, None, None, p, p, p, 16, 64, 256, 8, 2, 0, 1, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_INVALID and "scale" in cm.last_error()
+    rc = L.candle_moe_fused_moe_fp8(p, p, None, None, p, p, None, p, p, p, 16, 64, 256, 8, 2, 0, 1, 1, None)
+    assert rc == cm.CANDLE_MOE_ERR_INVALID and "null tensor pointer" in cm.last_error()
+    assert L.candle_moe_fused_moe_fp8(None, None, None, None, None, None, None, None, None, None, 0, 64, 256, 8, 2,
+                                      0, 0, 1, None) == cm.CANDLE_MOE_OK
+    assert L.candle_moe_quantize_fp8(p, 3, 1, 16, 16, 1, p, p, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_quantize_fp8(None, 1, 1, 16, 16, 1, p, p, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_quantize_fp8(None, 1, 0, 16, 16, 1, None, None, None) == cm.CANDLE_MOE_OK
+    assert L.candle_moe_dequantize_fp8(p, None, 1, 16, 16, p, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+    assert L.candle_moe_dequantize_fp8(p, p, 1, -1, 16, p, 1, None) == cm.CANDLE_MOE_ERR_INVALID

@@ -1,0 +1,149 @@
+"""FP8 expert weights on the GPU (candle_moe_quantize_fp8 / _dequantize_fp8 /
+_fused_moe_fp8) against the CPU oracle.
+
+* dequantize: all 256 codes bit-exact against the oracle's decode (itself
+  pinned to the OCP e4m3 definition by tests/test_fp8_oracle.py);
+* quantize: codes and scales bit-exact against the oracle's quantizer, both
+  input layouts, f32/f16/bf16, with planted zero channels, ties and
+  saturating values;
+* fused_moe_fp8: against the oracle's f64 MoE over the dequantized weights
+  (decode(q) * scale in f32), at the tolerance of the activation dtype
+  (rtol 1e-2 f16, 2e-2 bf16, atol = rtol * RMS), at the decode shapes of
+  Qwen3 (H4096 I1536 E8 k2, T = 8..64), Qwen3-30B-A3B (H2048 I768 E128 k8,
+  T = 1, 16) and Nomic (H768 I3072 E8 k2 GELU), and in accumulate mode.
+"""
+import numpy as np
+import pytest
+
+import candle_moe
+import oracle as O
+from helpers import RTOL, assert_close, from_dev, moe_inputs, to_dev, torch_dtype
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+def test_dequantize_all_codes_bit_exact():
+    import torch
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(1, 1, 256).cuda()
+    ones = torch.ones((1, 1), dtype=torch.float32, device="cuda:0")
+    got = _np(candle_moe.dequantize_fp8(codes, ones, torch.float32)).ravel()
+    want = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))  # signed zeros included
+    # scaled, rounded to the 16-bit dtypes
+    sc = np.array([[0.3712]], np.float32)
+    prod = (want * sc[0, 0]).astype(np.float32)
+    for dt in (O.BF16, O.F16):
+        out = candle_moe.dequantize_fp8(codes, torch.from_numpy(sc).cuda(), torch_dtype(dt))
+        g = from_dev(out).ravel()
+        w = O.round_to(prod, dt)
+        assert np.array_equal(np.isnan(g), np.isnan(w))
+        assert np.array_equal(g[fin], w[fin])
+
+
+def _planted_weights(E, K, N, dt, seed):
+    w = O.randn((E, K, N), seed=seed, std=0.05)
+    w[0, :, 1] = 0.0                                   # zero channel
+    w[1, 3, 2] = 7.0                                   # dominant element
+    w[E - 1, :, N - 1] = np.float32(2.0 ** -10)        # a channel of one repeated value
+    # values at midpoints of the e4m3 grid after scaling by max/448 = 1 (channel max 448)
+    w[0, 0, 3] = 448.0
+    w[0, 1:9, 3] = np.array([0.5625, 1.0625, 1.1875, 3 * 2.0 ** -11, 2.0 ** -10, 17.0, 232.0, -9.5], np.float32)
+    return O.to_dtype(w, dt)
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
+@pytest.mark.parametrize("kn", [True, False])
+def test_quantize_matches_oracle_bit_exact(dt, kn):
+    E, K, N = 3, 200, 72
+    ws = _planted_weights(E, K, N, dt, seed=40 + dt)
+    if not kn:
+        ws = np.ascontiguousarray(np.transpose(ws, (0, 2, 1)))
+    q, s = candle_moe.quantize_fp8(to_dev(ws, dt), input_kn=kn)
+    qo, so = O.quantize_fp8(ws, dt, kn=kn)
+    assert np.array_equal(_np(s), so)
+    assert np.array_equal(_np(q), qo)
+
+
+# the decode shapes: (name, T, H, I, E, k, act, moe_type, dt, zipf)
+CASES = [
+    ("qwen3_T8", 8, 4096, 1536, 8, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("qwen3_T16", 16, 4096, 1536, 8, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("qwen3_T32", 32, 4096, 1536, 8, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("qwen3_T64", 64, 4096, 1536, 8, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("qwen3_T16_f16", 16, 4096, 1536, 8, 2, O.SILU, O.QWEN3, O.F16, 0.0),
+    ("qwen3_30b_T1", 1, 2048, 768, 128, 8, O.SILU, O.QWEN3, O.BF16, 1.1),
+    ("qwen3_30b_T16", 16, 2048, 768, 128, 8, O.SILU, O.QWEN3, O.BF16, 1.1),
+    ("nomic_T16", 16, 768, 3072, 8, 2, O.GELU, O.NOMIC, O.BF16, 0.0),
+    ("nomic_T16_f16", 16, 768, 3072, 8, 2, O.GELU, O.NOMIC, O.F16, 0.0),
+    ("qwen3_odd_T5", 5, 272, 208, 4, 2, O.RELU, O.QWEN3, O.BF16, 0.0),  # sizes off the 64-element tiles
+]
+
+
+def _quantized_case(T, H, I, E, k, moe_type, dt, zipf, seed):
+    """Inputs, the GPU-quantized weights (checked against the oracle's
+    quantizer) and the dequantized f32 weights in the oracle's layouts."""
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, seed, moe_type, zipf_s=zipf)
+    dev = {}
+    deq = {}
+    # Qwen3: gate/up [E,H,I] and down [E,I,H] are [E,K,N]; Nomic: fc1 [E,H,I]
+    # is [E,K,N], fc2 [E,H,I] is [E,N,K]
+    specs = [("g", G, True), ("u", U, moe_type == O.QWEN3)] + ([("d", D, True)] if moe_type == O.QWEN3 else [])
+    for name, w, kn in specs:
+        q, s = candle_moe.quantize_fp8(to_dev(w, dt), input_kn=kn)
+        qo, so = O.quantize_fp8(w, dt, kn=kn)
+        assert np.array_equal(_np(q), qo) and np.array_equal(_np(s), so), f"quantize {name}"
+        dev[name] = (q, s)
+        d = O.dequantize_fp8(qo, so)  # [E,N,K]
+        deq[name] = np.ascontiguousarray(np.transpose(d, (0, 2, 1))) if kn else d
+    return x, rw, ri, dev, deq
+
+
+def _run_fp8(x, rw, ri, dev, E, k, act, moe_type, dt, out_init=None):
+    import torch
+
+    T, H = x.shape
+    tx = to_dev(x, dt)
+    out = torch.zeros((T, H), dtype=tx.dtype, device="cuda:0") if out_init is None else to_dev(out_init, dt)
+    g, u = dev["g"], dev["u"]
+    if moe_type == O.QWEN3:
+        d = dev["d"]
+        candle_moe.fused_moe_fp8(tx, g[0], u[0], d[0], g[1], u[1], d[1], to_dev(rw), to_dev(ri), out, E, k, act,
+                                 moe_type)
+    else:  # fc1 = gate, fc2 = up
+        candle_moe.fused_moe_fp8(tx, g[0], u[0], None, g[1], u[1], None, to_dev(rw), to_dev(ri), out, E, k, act,
+                                 moe_type)
+    torch.cuda.synchronize()
+    return from_dev(out).astype(np.float64)
+
+
+def _oracle(x, rw, ri, deq, E, k, act, moe_type, dt, out_init=None):
+    xf = O.to_f32(x, dt)
+    oi = None if out_init is None else O.to_f32(out_init, dt).astype(np.float64)
+    return O.fused_moe(xf, deq["g"], deq["u"], deq.get("d"), rw, ri, E=E, k=k, act=act, moe_type=moe_type,
+                       dtype=O.F32, mode=O.MODE_EXACT, out_init=oi)
+
+
+@pytest.mark.parametrize("name,T,H,I,E,k,act,mt,dt,zipf", CASES, ids=[c[0] for c in CASES])
+def test_fused_moe_fp8_matches_oracle(name, T, H, I, E, k, act, mt, dt, zipf):
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, zipf, seed=50 + T)
+    got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
+    assert_close(got, want, RTOL[dt], f"{name} fp8 vs f64 oracle on the dequantized weights")
+
+
+@pytest.mark.parametrize("mt", [O.QWEN3, O.NOMIC])
+def test_fused_moe_fp8_accumulates(mt):
+    T, H, I, E, k = (16, 4096, 1536, 8, 2) if mt == O.QWEN3 else (16, 768, 3072, 8, 2)
+    act = O.SILU if mt == O.QWEN3 else O.GELU
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, O.BF16, 0.0, seed=77)
+    init = O.to_dtype(O.randn((T, H), seed=78, std=0.5), O.BF16)
+    got = _run_fp8(x, rw, ri, dev, E, k, act, mt, O.BF16, out_init=init)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, O.BF16, out_init=init)
+    assert_close(got, want, RTOL[O.BF16], "fp8 accumulate mode")
