@@ -382,6 +382,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         auto bound = [&](int K) { return std::max(1, std::min(8, cdiv(K, bk))); };
         if (!p.set_path) p.split2 = bound(I);
         p.split1 = bound(H);
+#ifndef CM_W8_SPLITX
+#define CM_W8_SPLITX 1
+#endif
+        if (fp8) p.split_target = (int)(p.split_target * (CM_W8_SPLITX));
     } else if (is_f32_cfg(p.cfg) && P > 0) {
         const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);

@@ -55,6 +55,17 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
+// Wait for the DMA of the stage that has `newer` stages (of LOADS
+// instructions each) issued after it; at most MAXN of them can be.
+template <int LOADS, int MAXN>
+__device__ __forceinline__ void wait_stage(int newer) {
+    if constexpr (MAXN <= 0) {
+        wait_vm<0>();
+    } else {
+        if (newer >= MAXN) wait_vm<MAXN * LOADS>();
+        else wait_stage<LOADS, MAXN - 1>(newer);
+    }
+}
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" : : : "memory"); }
 
@@ -115,20 +126,24 @@ __device__ __forceinline__ u32x4 tr_pair(const char* p_lo, const char* p_hi) {
 }
 
 // Eight OCP fp8 e4m3 values (bytes of v, lowest first) as the MFMA operand of
-// the activation dtype: v_cvt_pk_f32_fp8 decodes two bytes to f32 (every
-// e4m3 value is exact in bf16 and f16, so the packing conversion is exact).
+// the activation dtype, exactly (every e4m3 value is a bf16 and an f16): the
+// gfx950 scaled conversion with scale 1 turns the two bytes of one 16-bit
+// word into a DT pair, low byte in the low half (one instruction per pair
+// instead of an f32 decode and a packing conversion).
 template <int DT>
 __device__ __forceinline__ u32x4 fp8x8_to(const u32x2& v) {
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], false);
-    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], true);
-    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], false);
-    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], true);
     u32x4 r;
-    r[0] = pack2<DT>(a[0], a[1]);
-    r[1] = pack2<DT>(b[0], b[1]);
-    r[2] = pack2<DT>(c[0], c[1]);
-    r[3] = pack2<DT>(d[0], d[1]);
+    if constexpr (DT == kBF16) {
+        r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.0f, false));
+        r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.0f, true));
+        r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.0f, false));
+        r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.0f, true));
+    } else {
+        r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[0], 1.0f, false));
+        r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[0], 1.0f, true));
+        r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[1], 1.0f, false));
+        r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[1], 1.0f, true));
+    }
     return r;
 }
 
@@ -147,7 +162,9 @@ __device__ __forceinline__ u32x4 fp8x8_to(const u32x2& v) {
 // read-after-write hazards only the compiler knows to pad.
 constexpr int kCachePolicyDevice = 16;  // CPol::SC1
 
-template <int MB, int NB, int NW, int BATCH>
+// PAIRED: the partials of two splits are loaded per round (the 32-row
+// kernels, whose fixup is a chain of round trips at decode sizes).
+template <int MB, int NB, int NW, int BATCH, bool PAIRED = false>
 __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB][NB], int slot0, int ctr, int ks,
                                              int nsplit, int wave, int lane) {
     __shared__ int s_last;
@@ -195,8 +212,39 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB
             }
         }
     };
-    gather(0, std::true_type{});
-    for (int s2 = 1; s2 < nsplit; ++s2) gather(s2, std::false_type{});
+    if constexpr (PAIRED) {
+        // splits s2 and s2 + 1 in flight together, summed in split order
+        auto gather2 = [&](int s2, auto first) {
+            const uint32_t src0 = (uint32_t)(slot0 + s2) * (uint32_t)PER * 4u + lane_off;
+            const uint32_t src1 = src0 + (uint32_t)PER * 4u;
+            const bool two = s2 + 1 < nsplit;
+            u32x4 v0[NQ], v1[NQ];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) v0[q] = __builtin_amdgcn_raw_buffer_load_b128(pr, src0 + q * 1024, 0, kCachePolicyDevice);
+            if (two) {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+                    v1[q] = __builtin_amdgcn_raw_buffer_load_b128(pr, src1 + q * 1024, 0, kCachePolicyDevice);
+            }
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                f32x16& r = acc[(q >> 2) / NB][(q >> 2) % NB];
+                const int i = 4 * (q & 3);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float x = __uint_as_float(v0[q][j]);
+                    if constexpr (decltype(first)::value) r[i + j] = x;
+                    else r[i + j] += x;
+                    if (two) r[i + j] += __uint_as_float(v1[q][j]);
+                }
+            }
+        };
+        gather2(0, std::true_type{});
+        for (int s2 = 2; s2 < nsplit; s2 += 2) gather2(s2, std::false_type{});
+    } else {
+        gather(0, std::true_type{});
+        for (int s2 = 1; s2 < nsplit; ++s2) gather(s2, std::false_type{});
+    }
     if (threadIdx.x == 0) __hip_atomic_store(a.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
 }
@@ -269,7 +317,8 @@ __device__ __forceinline__ int decode_set(int key, int k_top, int n_experts, int
 //  kDown / kFc2   : acc_f32[tok] += w * acc            (f32 atomics)
 //  kDownRows / kFc2Rows: rows[p] = dtype(w * acc)      (the pair's own row)
 // sc0 / sc1 (fp8 weights, else null): per-output-column scales of the
-// tile's expert (gate / up for kGateUp), applied to the f32 sums first.
+// tile's expert (gate / up for kGateUp), indexed from the tile's first column
+// (nt * BN, or nt * BN/2 for kGateUp), applied to the f32 sums first.
 template <int DT, int MODE, int BN, int WM, int WN, int MB, int NB>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], int r0, int m_valid, int nt,
                                               int wm, int wn, int lane, const int32_t* s_tok, const float* s_w,
@@ -285,7 +334,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int col = nt * BN + wn * WN + nb * 32 + lr;
-            cs[nb] = (sc0 && col < N) ? sc0[col] : 1.0f;
+            cs[nb] = sc0 ? sc0[col - nt * BN] : 1.0f;
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
@@ -336,9 +385,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
                                 // (fp8 weights: the column scales first)
-                                const float s0 = sc0 ? sc0[col + j] : 1.0f;
+                                const int cj = col + j - (DUAL ? nt * (BN / 2) : nt * BN);
+                                const float s0 = sc0 ? sc0[cj] : 1.0f;
                                 if constexpr (DUAL) {
-                                    const float s1 = sc1 ? sc1[col + j] : 1.0f;
+                                    const float s1 = sc1 ? sc1[cj] : 1.0f;
                                     h[j] = act_t<ACT>(s0 * acc[mb][2 * q][4 * g + j]) * (s1 * acc[mb][2 * q + 1][4 * g + j]);
                                 } else {
                                     h[j] = act_t<ACT>(s0 * acc[mb][q][4 * g + j]);

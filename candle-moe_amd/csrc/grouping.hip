@@ -216,7 +216,6 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem) {
     int32_t* s_tb = s_tot + nbins;
     int32_t* s_base = s_tb + nbins;
     int32_t* s_part = s_base + nbins;
-    const int ncounts = nblocks * nbins;  // < 2^31 (checked by the launcher)
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const long long wbase = (long long)blk * kGroupChunk + wave * 64 * IPT;

@@ -84,6 +84,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
     __shared__ int32_t s_tok[(ATOMIC || SET) ? BM : 1];
     __shared__ float s_w[ATOMIC ? BM : 1];
+    __shared__ float s_sc[W8 ? BN : 1];
 
     // workgroup -> (output tile, K split); every workgroup first clears its
     // share of zero_f32 (the accumulator of the GEMM that follows)
@@ -168,6 +169,17 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             const int col = nt * SUBN + c * 8;
             b_off[i] = col < N ? ((uint32_t)col + (uint32_t)r * (uint32_t)a.ldb) * 2u : kOob;
         }
+    }
+
+    // fp8 weights: this thread's column scale of the tile (256 threads, 256
+    // columns: gate then up for kGateUp), loaded now, staged in LDS for the
+    // epilogue after the K loop
+    float sc_pre = 1.0f;
+    if constexpr (W8) {
+        static_assert(BN == 64 * NW, "one scale per thread");
+        const int c = DUAL ? nt * SUBN + tid % SUBN : nt * BN + tid;
+        const float* src = (DUAL && tid >= SUBN) ? a.scale1 : a.scale0;
+        if (c < N) sc_pre = src[(long long)grp * N + c];
     }
 
     // Weight buffer resources of the current expert; on the expert-set path
@@ -293,14 +305,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            if constexpr (W8) {
-                // 8 fp8 weights (k = 16 kk + 8 lh .. +7 of n-row r), converted
-                // exactly to the activation dtype
-                const int sub = DUAL ? (nb & 1) : 0;
-                const int r = DUAL ? wn * (WN / 2) + (nb >> 1) * 32 + lr : wn * WN + nb * 32 + lr;
-                const char* q8 = sB + sub * W8_SUB_BYTES + r * KROW + a_swz<KCH>(r, kk) * 16 + lh * 8;
-                bfr[nb] = fp8x8_to<DT>(*reinterpret_cast<const u32x2*>(q8));
-            } else if constexpr (BNK) {
+            if constexpr (BNK) {
                 const int r = wn * WN + nb * 32 + lr;
                 bfr[nb] = *reinterpret_cast<const u32x4*>(sB + r * AROW + a_swz<ACH>(r, c) * 16);
             } else {
@@ -351,7 +356,46 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // group) reads no fragments and issues no MFMAs; it still issues its DMA
     // share and meets every barrier. On a half-empty tile this leaves the
     // matrix core of each SIMD to the other wave.
-    const bool rows_live = wm * WM < m_valid;
+    // (one wave row: every wave holds the tile's rows, and m_valid >= 1; as a
+    // constant the compiler keeps the accumulators in place across the loop)
+    const bool rows_live = WGM == 1 || wm * WM < m_valid;
+    // fp8 weights: all LDS reads of a stage first (A fragments and the raw
+    // fp8 bytes of every k16 step), then per step the conversion and the
+    // MFMAs, so that the LDS latency of later steps runs under the
+    // conversions and MFMAs of earlier ones (converting right after each read
+    // serialises read, wait, conversion and MFMA step by step).
+    auto compute_w8 = [&](int stage) {
+        if (!rows_live) return;
+        const char* sA = smem + stage * STAGE;
+        const char* sB = sA + A_BYTES;
+        u32x4 af[KSTEPS][MB];
+        u32x2 braw[KSTEPS][NB];
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+            const int c = kk * 2 + lh;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int r = a_frag_row[mb];
+                af[kk][mb] = *reinterpret_cast<const u32x4*>(sA + r * AROW + a_swz<ACH>(r, c) * 16);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int sub = DUAL ? (nb & 1) : 0;
+                const int r = DUAL ? wn * (WN / 2) + (nb >> 1) * 32 + lr : wn * WN + nb * 32 + lr;
+                // 8 fp8 weights: k = 16 kk + 8 lh .. +7 of n-row r
+                braw[kk][nb] = *reinterpret_cast<const u32x2*>(sB + sub * W8_SUB_BYTES + r * KROW +
+                                                                a_swz<KCH>(r, kk) * 16 + lh * 8);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every read issued before the first conversion
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+            u32x4 bfr[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) bfr[nb] = fp8x8_to<DT>(braw[kk][nb]);  // exact in DT
+            mfma_step(af[kk], bfr);
+        }
+    };
     auto compute = [&](int stage, int ds, int dk) {
         if (!rows_live) {
 #pragma unroll
@@ -429,7 +473,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     const int kt0 = min(nk_all, ks * per_split);
     const int nk = min(nk_all, kt0 + per_split) - kt0;
 
-    if constexpr (NW == 4 && !GATHER) {
+    if constexpr (NW == 4 && !GATHER && !W8) {
         // 4-wave down / fc2 kernels: hand-over one k16 step early. The
         // barrier of tile kt+1 sits before the MFMAs of tile kt's last k16
         // step, whose fragments are already in registers, so the MFMAs issued
@@ -446,18 +490,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         //   tile kt's last step.
         // wait for the DMA of the tile with `newer` of this wave's tiles
         // issued after it
-        auto wait_tile = [&](int newer) {
-            if constexpr (NST >= 4) {
-                if (newer >= 2) wait_vm<2 * LOADS>();
-                else if (newer == 1) wait_vm<LOADS>();
-                else wait_vm<0>();
-            } else if constexpr (NST == 3) {
-                if (newer >= 1) wait_vm<LOADS>();
-                else wait_vm<0>();
-            } else {
-                wait_vm<0>();
-            }
-        };
+        auto wait_tile = [&](int newer) { wait_stage<LOADS, NST - 2>(newer); };
         u32x4 af0[MB], bf0[NB], af1[MB], bf1[NB];
 #pragma unroll
         for (int s = 0; s < NST - 1; ++s)
@@ -509,41 +542,37 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         if (s < nk) issue(s, (kt0 + s) * BK);
     for (int kt = 0; kt < nk; ++kt) {
         const int newer = min(NST - 2, nk - 1 - kt);  // stages issued after kt and before this wait
-        if constexpr (NST >= 4) {
-            if (newer >= 2) wait_vm<2 * LOADS>();
-            else if (newer == 1) wait_vm<LOADS>();
-            else wait_vm<0>();
-        } else if constexpr (NST == 3) {
-            if (newer >= 1) wait_vm<LOADS>();
-            else wait_vm<0>();
-        } else {
-            wait_vm<0>();
-        }
+        wait_stage<LOADS, NST - 2>(newer);
         wait_lgkm0();
         block_barrier();
         const int ahead = kt + NST - 1;
         const bool late = NW == 8 && wm == 1;  // row group 1 issues after its first k16 step
         if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
-        compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
+        if constexpr (W8) compute_w8(kt % NST);
+        else compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
     }
     }
 
     if constexpr (FIXUP) {
         // split K: the last split to finish a tile sums all partials in split
         // order and alone runs the epilogue (one atomic per output element and
-        // pair, as without splits)
+        // pair, as without splits: the result does not depend on the order in
+        // which splits finish)
         // loads in flight per batch: the atomic-combine kernels keep their
         // row table in registers and have less room
         constexpr int FIX_BATCH = ATOMIC ? 4 : 8;
-        if (nsplit > 1 && !splitk_fixup<MB, NB, NW, FIX_BATCH>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
+        if (nsplit > 1 &&
+            !splitk_fixup<MB, NB, NW, FIX_BATCH, (BM <= 32)>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
             return;
     }
-    // fp8 weights: per-output-channel scales of this tile's expert
+    // fp8 weights: the tile's column scales, staged in LDS
     const float* sc0 = nullptr;
     const float* sc1 = nullptr;
     if constexpr (W8) {
-        sc0 = a.scale0 + (long long)grp * N;
-        if constexpr (DUAL) sc1 = a.scale1 + (long long)grp * N;
+        s_sc[tid] = sc_pre;
+        __syncthreads();
+        sc0 = s_sc;
+        if constexpr (DUAL) sc1 = s_sc + SUBN;
     }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
                                                 (GATHER || ROWS) ? pre_dst : nullptr,
@@ -593,8 +622,14 @@ static hipError_t launch_w8_mode(const GemmArgs& a, hipStream_t stream) {
     const long long nwg_l = split_grid(tiles, a);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     if (nwg_l <= 0) return hipSuccess;
-    hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1, 1, true>), dim3((int)nwg_l), dim3(256), 0, stream,
-                       a);
+#ifndef CM_W8_NST
+#define CM_W8_NST 4
+#endif
+#ifndef CM_W8_OCC
+#define CM_W8_OCC 1
+#endif
+    hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, CM_W8_NST, 4, MODE, 1, CM_W8_OCC, true>), dim3((int)nwg_l),
+                       dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 template <int DT>
