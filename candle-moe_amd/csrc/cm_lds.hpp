@@ -450,5 +450,93 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
     }
 }
 
+// Epilogue through LDS for the large-tile kernels (gate/up, fc1, expert-set
+// down / fc2 with overwrite, pair-row down / fc2). In the swapped MFMA layout
+// a lane holds 4-column pieces of one tile row, so direct stores put 16
+// bytes into each of 32 rows per instruction. Instead: (1) every wave writes
+// its finished values, converted to DT, into a [BM][W] tile in the stage
+// buffers (row-major, 16-byte chunk c of row r at c ^ (r % CPR), so that the
+// 32 rows of a write and the chunks of a row read land in distinct banks);
+// (2) the waves store whole rows, 16 bytes per lane, CPR lanes per row.
+// dst_rows[r]: output row of tile row r; rows >= m_valid are not stored.
+template <int DT, int MODE, int BM, int BN, int WM, int WN, int MB, int NB, int NW>
+__device__ __forceinline__ void staged_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], char* tile_lds,
+                                                const int32_t* dst_rows, int m_valid, int nt, int wm, int wn,
+                                                int lane, const float* pre_w) {
+    constexpr bool DUAL = (MODE == kGateUp);
+    constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
+    constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
+    constexpr int W = DUAL ? BN / 2 : BN;  // output columns of the tile
+    constexpr int CPR = W / 8;             // 16-byte chunks per row
+    constexpr int RB = W * 2;              // bytes per row
+    static_assert(CPR == 8 || CPR == 16 || CPR == 32, "row chunks");
+    const int N = a.N;
+    const int lr = lane & 31, nsub = 4 * (lane >> 5);
+    auto put = [&](int ml, int lc, float h0, float h1, float h2, float h3) {
+        u32x2 v;
+        v[0] = pack2<DT>(h0, h1);
+        v[1] = pack2<DT>(h2, h3);
+        const int c = lc >> 3;
+        *reinterpret_cast<u32x2*>(tile_lds + ml * RB + ((c ^ (ml % CPR)) << 4) + (lc & 7) * 2) = v;
+    };
+    // (1) values into LDS
+    if constexpr (GATHER) {
+        with_act(a.act, [&](auto act_c) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int ml = wm * WM + mb * 32 + lr;
+                const float ws = pre_w[mb];
+                constexpr int PAIRS = DUAL ? NB / 2 : NB;
+#pragma unroll
+                for (int q = 0; q < PAIRS; ++q) {
+                    const int lbase = DUAL ? ((wn * WN) / 64 + q) * 32 : wn * WN + q * 32;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        float h[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            if constexpr (DUAL)
+                                h[j] = act_t<ACT>(acc[mb][2 * q][4 * g + j]) * acc[mb][2 * q + 1][4 * g + j];
+                            else
+                                h[j] = act_t<ACT>(acc[mb][q][4 * g + j]);
+                            h[j] *= ws;
+                        }
+                        put(ml, lbase + 8 * g + nsub, h[0], h[1], h[2], h[3]);
+                    }
+                }
+            }
+        });
+    } else {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int ml = wm * WM + mb * 32 + lr;
+            const float ws = ROWS ? pre_w[mb] : 1.0f;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int i = 4 * g;
+                    put(ml, wn * WN + nb * 32 + 8 * g + nsub, ws * acc[mb][nb][i], ws * acc[mb][nb][i + 1],
+                        ws * acc[mb][nb][i + 2], ws * acc[mb][nb][i + 3]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // (2) whole rows out
+    constexpr int RPI = 64 / CPR;  // rows per wave instruction
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane % CPR;
+    const int col = nt * W + c * 8;
+    uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+    if (col < N) {
+        for (int r = wave * RPI + lane / CPR; r < m_valid; r += NW * RPI) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(tile_lds + r * RB + ((c ^ (r % CPR)) << 4));
+            *reinterpret_cast<u32x4*>(C + (long long)dst_rows[r] * N + col) = v;
+        }
+    }
+}
+
 }  // namespace lds
 }  // namespace cm

@@ -85,6 +85,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     __shared__ int32_t s_tok[(ATOMIC || SET) ? BM : 1];
     __shared__ float s_w[ATOMIC ? BM : 1];
     __shared__ float s_sc[W8 ? BN : 1];
+    // staged (row-contiguous) epilogue of the large tiles, see staged_epilogue
+    constexpr bool STAGED = SWAP && !W8 && BM >= 128;
+    static_assert(!STAGED || NST * STAGE >= BM * (DUAL ? BN / 2 : BN) * 2, "output tile fits the stages");
+    __shared__ int32_t s_dst[STAGED ? BM : 1];
 
     // workgroup -> (output tile, K split); every workgroup first clears its
     // share of zero_f32 (the accumulator of the GEMM that follows)
@@ -573,6 +577,22 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         __syncthreads();
         sc0 = s_sc;
         if constexpr (DUAL) sc1 = s_sc + SUBN;
+    }
+    if constexpr (STAGED) {
+        if (!SET || a.overwrite) {
+            // output row of every tile row (gate/up, fc1: the pair's inter row;
+            // pair rows: the pair; expert sets: the token, already in s_tok)
+            if constexpr (GATHER || ROWS) {
+                if (wn == 0 && lane < 32) {
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) s_dst[wm * WM + mb * 32 + lane] = pre_dst[mb];
+                }
+            }
+            __syncthreads();  // every wave is done with the stages
+            staged_epilogue<DT, MODE, BM, BN, WM, WN, MB, NB, NW>(a, acc, smem, SET ? s_tok : s_dst, m_valid, nt, wm,
+                                                                 wn, lane, pre_w);
+            return;
+        }
     }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
                                                 (GATHER || ROWS) ? pre_dst : nullptr,
