@@ -15,7 +15,7 @@ runs on (candle_moe_profile_begin_slots: only that launch is bracketed in the
 timed region; the per-kernel breakdown comes from a separate untimed pass). `cpu_baseline` times the CPU oracle (the
 candle-native per-expert loop, a port) on a bounded token sample.
 
-    python bench.py [--steps K] [--warmup W] [--workload qwen3|nomic|q30b|router]
+    python bench.py [--steps K] [--warmup W] [--workload qwen3|nomic|q30b|router|fp8]
 """
 from __future__ import annotations
 
@@ -48,7 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + ["router"])
+    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + ["router", "fp8"],
+                    help="MoE layer (qwen3 headline, nomic, q30b), router alone, or fp8: the decode GEMMs with "
+                         "bf16 against fp8 expert weights only")
     ap.add_argument("--tokens", type=int, default=0, help="override T")
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
@@ -103,6 +105,13 @@ def main():
 
     if args.workload == "router":
         return bench_router_only(args, torch, cm, dev)
+    if args.workload == "fp8":
+        res = bench_fp8_decode(torch, cm, dev, args)
+        gu = [v["bf16"]["gemm_gate_up"] / v["fp8"]["gemm_gate_up"] for v in res.values()]
+        print(json.dumps({"metric": "decode GEMM time, bf16 over fp8 e4m3 expert weights", "value": round(min(gu), 3),
+                          "unit": "x (gate/up GEMM, worst shape)", "n_gpus": 1, "higher_is_better": True,
+                          "data": "synthetic", "config": {"workload": "fp8 decode GEMMs"}, "fp8_decode": res}))
+        return None
 
     wl = dict(WORKLOADS[args.workload])
     if args.tokens:

@@ -13,8 +13,9 @@
 // Layout: one group of LPR lanes per token row; lane g of the group owns
 // the VPT consecutive experts [g*VPT, g*VPT+VPT), loaded with 16-byte
 // vector loads, so a wave reads 64/LPR whole rows as one contiguous span.
-// Max, sum and argmax are butterflies over the group (DPP quad_perm,
-// ds_swizzle), so no LDS and no barriers are used.
+// Max, sum and the selection are butterflies over the group (DPP and
+// v_permlane16/32_swap lane exchanges, all VALU); LDS holds only the row of
+// probabilities the fast selection reads its weights back from.
 #include "cm_common.hpp"
 #include "cm_internal.hpp"
 #include "cm_lds.hpp"
