@@ -538,5 +538,68 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, f32x16 (&acc)
     }
 }
 
+// Expert-set down / fc2 in accumulate mode (out = dtype(out + acc), one
+// rounding from f32): as staged_epilogue, but the tile goes through LDS in
+// f32, half of its columns at a time (BM x BN/2 x 4 bytes fit the stages),
+// and each row store first reads the row's old values (16 bytes per lane).
+template <int DT, int BM, int BN, int WM, int WN, int MB, int NB, int NW>
+__device__ __forceinline__ void staged_epilogue_acc(const GemmArgs& a, f32x16 (&acc)[MB][NB], char* tile_lds,
+                                                    const int32_t* dst_rows, int m_valid, int nt, int wm, int wn,
+                                                    int lane) {
+    constexpr int HW = BN / 2;     // columns per half
+    constexpr int CPR = HW / 4;    // 16-byte (4 x f32) chunks per LDS row
+    constexpr int RB = HW * 4;     // bytes per LDS row
+    static_assert(CPR == 32, "half-tile rows");
+    static_assert(WN <= HW && HW % WN == 0, "a wave's columns lie in one half");
+    const int N = a.N;
+    const int lr = lane & 31, nsub = 4 * (lane >> 5);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (h) __syncthreads();  // the first half's rows are stored
+        // (1) the waves whose columns lie in this half write them, f32
+        if ((wn * WN) / HW == h) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int ml = wm * WM + mb * 32 + lr;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int lc = wn * WN - h * HW + nb * 32 + 8 * g + nsub;  // column in the half
+                        const int c = lc >> 2;
+                        u32x4 v;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) v[j] = __float_as_uint(acc[mb][nb][4 * g + j]);
+                        *reinterpret_cast<u32x4*>(tile_lds + ml * RB + ((c ^ (ml % CPR)) << 4)) = v;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // (2) rows: 16 lanes per row, 8 columns (two LDS chunks) per lane
+        const int c8 = lane & 15;
+        const int col = nt * BN + h * HW + c8 * 8;
+        if (col < N) {
+            for (int r = wave * 4 + (lane >> 4); r < m_valid; r += NW * 4) {
+                const u32x4 lo = *reinterpret_cast<const u32x4*>(tile_lds + r * RB + (((2 * c8) ^ (r % CPR)) << 4));
+                const u32x4 hi = *reinterpret_cast<const u32x4*>(tile_lds + r * RB + (((2 * c8 + 1) ^ (r % CPR)) << 4));
+                uint16_t* dst = C + (long long)dst_rows[r] * N + col;
+                const u32x4 old = *reinterpret_cast<const u32x4*>(dst);
+                u32x4 v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t o = old[q];
+                    const float x0 = Elem<DT>::to_f32((uint16_t)(o & 0xffffu)) + __uint_as_float(q < 2 ? lo[2 * q] : hi[2 * q - 4]);
+                    const float x1 = Elem<DT>::to_f32((uint16_t)(o >> 16)) + __uint_as_float(q < 2 ? lo[2 * q + 1] : hi[2 * q - 3]);
+                    v[q] = pack2<DT>(x0, x1);
+                }
+                *reinterpret_cast<u32x4*>(dst) = v;
+            }
+        }
+    }
+}
+
 }  // namespace lds
 }  // namespace cm

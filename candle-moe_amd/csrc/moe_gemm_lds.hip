@@ -593,6 +593,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                                                                  wn, lane, pre_w);
             return;
         }
+        if constexpr (SET && BN == 256 && NST * STAGE >= BM * (BN / 2) * 4) {
+            __syncthreads();  // every wave is done with the stages
+            staged_epilogue_acc<DT, BM, BN, WM, WN, MB, NB, NW>(a, acc, smem, s_tok, m_valid, nt, wm, wn, lane);
+            return;
+        }
     }
     tile_epilogue<DT, MODE, BN, WM, WN, MB, NB>(a, acc, r0, m_valid, nt, wm, wn, lane, s_tok, s_w,
                                                 (GATHER || ROWS) ? pre_dst : nullptr,
