@@ -147,3 +147,29 @@ def test_fused_moe_fp8_accumulates(mt):
     got = _run_fp8(x, rw, ri, dev, E, k, act, mt, O.BF16, out_init=init)
     want = _oracle(x, rw, ri, deq, E, k, act, mt, O.BF16, out_init=init)
     assert_close(got, want, RTOL[O.BF16], "fp8 accumulate mode")
+
+
+def test_fused_moe_fp8_drops_out_of_range_experts():
+    # expert ids >= E are dropped by the grouping, as on the bf16 path
+    T, H, I, E, k = 24, 512, 256, 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=91)
+    ri = ri.copy()
+    ri[::3, 1] = E + 5
+    ri[5, :] = 1000
+    got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16)
+    want = _oracle(x, rw, ri, deq, E, k, O.SILU, O.QWEN3, O.BF16)
+    assert not np.any(want[5]) and not np.any(got[5])
+    assert_close(got, want, RTOL[O.BF16], "fp8 with dropped pairs")
+
+
+def test_fused_moe_fp8_prefill_batch_sampled_rows():
+    # the fp8 entry point runs the 32-row kernel at every batch size: 2048
+    # tokens give ~128 row tiles per GEMM and no K splits
+    T, H, I, E, k = 2048, 1024, 512, 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=92)
+    got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16)
+    rows = list(range(0, T, 29)) + [T - 1]
+    xf = O.to_f32(x, O.BF16)
+    want = O.fused_moe(xf, deq["g"], deq["u"], deq["d"], rw, ri, E=E, k=k, act=O.SILU, moe_type=O.QWEN3,
+                       dtype=O.F32, mode=O.MODE_EXACT, rows=rows)
+    assert_close(got[rows], want, RTOL[O.BF16], "fp8 at T=2048 (sampled rows)")
