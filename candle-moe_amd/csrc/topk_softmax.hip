@@ -9,6 +9,10 @@
 // Numerics (shared with the CPU oracle so indices agree bit-exactly):
 //   exp is evaluated in f64 and rounded once to f32, the row sum is an f64
 //   sum rounded once to f32, and p = e / S is an IEEE f32 division.
+//   f32 weights over 64..256 experts take an f32 softmax first (exp within
+//   1 ulp, weights within 5.4e-7 of the above) and keep it for every row
+//   whose top k + 1 are far enough apart that the exact p order is the same;
+//   the other rows redo the exact softmax.
 //
 // Layout: one group of LPR lanes per token row; lane g of the group owns
 // the VPT consecutive experts [g*VPT, g*VPT+VPT), loaded with 16-byte
@@ -143,6 +147,25 @@ __device__ __forceinline__ float exp_f32_f64(float d) {
     for (int i = 4; i < 15; ++i) s = __builtin_fma(r, s, kExpCoef[i]);
     const double y = __builtin_ldexp(__builtin_fma(s, r, 1.0), (int)n);
     return d < -104.0f ? 0.0f : (float)y;
+}
+
+// e^d in f32 arithmetic for an f32 d <= 0, within 1 ulp of the correctly
+// rounded value wherever that is a normal number (d >= -87.33; checked on the
+// GPU against exp_f32_f64 for every f32 d in that range: 96.7 % equal, the
+// rest 1 ulp apart). t = d log2(e) is carried as th + tl: th = f32(d L) with
+// L = f32(log2 e), tl = the product's rounding error (an exact fma) plus
+// d (log2 e - L); then 2^t = 2^th (1 + tl ln 2) to first order, |tl| being
+// below 2^-16. 2^th is the hardware v_exp_f32. Below the normal range the
+// result is approximate (possibly 0); below -104 it is +0, as above.
+__device__ __forceinline__ float exp_f32_fast(float d) {
+#pragma clang fp contract(off)
+    constexpr float L = 1.44269504088896341f;        // log2(e) rounded to f32
+    constexpr float Llo = 1.9259629911783648e-08f;   // log2(e) - L
+    constexpr float LN2 = 0.693147180559945309f;
+    const float th = d * L;
+    const float tl = __builtin_fmaf(d, Llo, __builtin_fmaf(d, L, -th));
+    const float y = __builtin_amdgcn_exp2f(th);
+    return d < -104.0f ? 0.0f : __builtin_fmaf(y, tl * LN2, y);
 }
 
 template <int VPT, int INDT>
@@ -334,6 +357,159 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
 #pragma unroll
     for (int r = 0; r < R; ++r) m[r] = group_max<LPR>(m[r]);
 
+    typedef typename Elem<OUTDT>::storage WS;
+    WS* wo = reinterpret_cast<WS*>(wout);
+    auto put = [&](long long rw, int j, float v, int e) {
+        const long long o = rw * (long long)k + j;
+        wo[o] = Elem<OUTDT>::from_f32(v);
+        iout[o] = (uint32_t)e;
+        eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)rw;
+    };
+
+    // f32 weights over 64 to 256 experts (8 per lane, whole rows): the
+    // softmax in f32 arithmetic first. e = exp_f32_fast(x - max) (within 1 ulp
+    // of the correctly rounded e), S = the f64 sum of those e, p = e * rcp(S).
+    // Against the exact p (f32(exp_f64), f64 sum rounded to f32, correctly
+    // rounded quotient) each p is within 6e-7 relative (e 1 ulp; S 2.4e-7
+    // after both roundings; the reciprocal 1 ulp; the product's and the exact
+    // p's roundings 0.6e-7 each), inside the 1e-6 weight tolerance.
+    // Selection: k + 1 passes over the lanes' sorted 32-bit keys (as in the
+    // exact path below) give the candidates, positions 0 .. c - 1 (c = k + 1)
+    // of the key order, lane j of the group keeping position j; the group's
+    // next key (position c) is the first expert left out. The top k in the
+    // exact order are the candidates' top k when
+    //  * position c's key lies at least two units of the key's upper bits
+    //    (2^IB ulps each) below position c - 1's: every expert left out then
+    //    has p smaller by more than 7.6e-6 relative than every candidate (up
+    //    to two more passes move the boundary down when it is not, while
+    //    lanes are left to hold the extra candidates);
+    //  * no two neighbouring candidates have p within 2e-6 relative (nor in
+    //    the wrong order, which the keys allow inside one unit): the exact p
+    //    are then ordered as these, being within 6e-7 of them;
+    // and the candidates' p are >= 2^-100 (normal e, where the 1-ulp bound
+    // holds) and the row is finite. Candidates closer than 2e-6 are ranked
+    // by their exact e instead (exp_f32_f64, one per lane), e descending,
+    // then the lower expert: p = f32(e / S) with one S for the row is equal
+    // for equal e and ordered like e where the e differ by two ulps or more;
+    // where they differ by one ulp and the larger e has the higher expert
+    // index, equal p (and the lower index first) depends on the exact S.
+    // That case, a boundary still too close after the extra passes, tiny p
+    // and non-finite rows send the wave to the exact softmax below.
+    if constexpr (R == 1 && VPT == 8 && LPR >= 8 && LPR * VPT <= 256 && OUTDT == kF32) {
+        if (s_row != nullptr && k < LPR && E == LPR * VPT) {
+            constexpr int IB = 32 - __builtin_clz(LPR * VPT - 1);
+            constexpr uint32_t MASK = (1u << IB) - 1u;
+            constexpr uint32_t TWO_UNITS = 2u << IB;
+            constexpr float PMIN = 7.88860905e-31f;  // 2^-100
+            constexpr float DELTA = 2e-6f;
+            const int lane = (int)(threadIdx.x & 63u);
+            const float mf = m[0];
+            float pf[VPT];
+            double sf = 0.0;
+#pragma unroll
+            for (int q = 0; q < VPT; ++q) {
+                pf[q] = exp_f32_fast(x[0][q] - mf);
+                sf += (double)pf[q];
+            }
+            sf = group_sum<LPR>(sf);
+            const float sff = (float)sf;
+            const float inv = __builtin_amdgcn_rcpf(sff);
+#pragma unroll
+            for (int q = 0; q < VPT; ++q) {
+                pf[q] *= inv;
+                s_row[e0 + q * ESTR] = pf[q];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            uint32_t key[VPT];
+#pragma unroll
+            for (int q = 0; q < VPT; ++q)
+                key[q] = ((__float_as_uint(pf[q]) | MASK) - (uint32_t)(e0 + q * ESTR)) + 1u;
+            sort_keys32<VPT>(key);
+            uint32_t mine = 0u;  // lane j of the group: the key at position j
+            // the group's largest remaining key (every lane of the group gets it)
+            auto top = [&]() { return group_key32_max<LPR>(key[0]); };
+            // its owner drops it
+            auto drop = [&](uint32_t best) {
+                const uint64_t pop = __builtin_amdgcn_ballot_w64(key[0] == best);
+#pragma unroll
+                for (int q = 0; q + 1 < VPT; ++q) key[q] = key_take32(key[q], key[q + 1], pop);
+                key[VPT - 1] = key_take32(key[VPT - 1], 0u, pop);
+            };
+            // key b two units of the upper bits below key a (both >= 1)
+            auto far_below = [&](uint32_t a, uint32_t b) {
+                const uint32_t ua = (a - 1u) | MASK, ub = (b - 1u) | MASK;
+                return ua >= TWO_UNITS && ub <= ua - TWO_UNITS;
+            };
+            int c = k + 1;
+            uint32_t last = 0u;
+            for (int j = 0; j < c; ++j) {
+                const uint32_t best = top();
+                drop(best);
+                mine = g == j ? best : mine;
+                last = best;
+            }
+            // the boundary: position c's key (not stored) against position
+            // c - 1's; while too close, position c joins the candidates
+            uint32_t next = top();
+            uint64_t open = __builtin_amdgcn_ballot_w64(!far_below(last, next));
+            for (int ext = 0; ext < 2 && open != 0ull && c < LPR; ++ext) {
+                drop(next);
+                mine = g == c ? next : mine;
+                ++c;
+                last = next;
+                next = top();
+                open = __builtin_amdgcn_ballot_w64(!far_below(last, next));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int ej = (int)(MASK - ((mine - 1u) & MASK));  // lane j < c: candidate j's expert
+            const float pj = s_row[ej];
+            // p of candidate g - 1 (lane g - 1 of the group; lane 0: its own)
+            const int prev_addr = (lane - (g > 0 ? 1 : 0)) << 2;
+            const float pprev = __int_as_float(__builtin_amdgcn_ds_bpermute(prev_addr, __float_as_int(pj)));
+            const bool near = g >= 1 && g < c && !(pprev - pj >= DELTA * pprev);
+            const bool bad = (g < c && !(pj >= PMIN)) || !(sff <= 3.0e38f);
+            const uint64_t any_near = __builtin_amdgcn_ballot_w64(near);
+            const uint64_t any_bad = __builtin_amdgcn_ballot_w64(bad);
+            if (open == 0ull && any_bad == 0ull) {
+                if (any_near == 0ull) {
+                    if (valid[0] && g < k) put(row[0], g, pj, ej);
+                    return;
+                }
+                // rank the candidates by exact e: the row's logits into the
+                // row buffer (its p are read), each candidate's exact e, then
+                // (e, expert) pairs at the buffer's start
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int q = 0; q < VPT; ++q) s_row[e0 + q * ESTR] = x[0][q];
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                const float ee = exp_f32_f64(s_row[ej] - mf);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (g < c) {
+                    s_row[2 * g] = ee;
+                    s_row[2 * g + 1] = __int_as_float(ej);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                int rank = 0;
+                bool amb = false;
+                for (int i = 0; i < c; ++i) {
+                    const float ei = s_row[2 * i];
+                    const int xi = __float_as_int(s_row[2 * i + 1]);
+                    rank += (ei > ee || (ei == ee && xi < ej)) ? 1 : 0;
+                    amb = amb || (__float_as_uint(ei) == __float_as_uint(ee) + 1u && xi > ej);
+                }
+                if (__builtin_amdgcn_ballot_w64(g < c && amb) == 0ull) {
+                    if (valid[0] && g < c && rank < k) put(row[0], rank, pj, ej);
+                    return;
+                }
+            }
+        }
+    }
+
     float p[R][VPT];
     double s[R];
 #pragma unroll
@@ -359,14 +535,6 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
         for (int j = 0; j < VPT; ++j) p[r][j] = (float)((double)p[r][j] * inv);
     }
 
-    typedef typename Elem<OUTDT>::storage WS;
-    WS* wo = reinterpret_cast<WS*>(wout);
-    auto put = [&](long long rw, int j, float v, int e) {
-        const long long o = rw * (long long)k + j;
-        wo[o] = Elem<OUTDT>::from_f32(v);
-        iout[o] = (uint32_t)e;
-        eiout[o] = (uint32_t)j * (uint32_t)T + (uint32_t)rw;
-    };
     // Fast selection on 32-bit keys (R == 1 with an LDS row buffer, k <= LPR): the key
     // of expert e is p's bits with the low IB bits replaced by MASK - e, plus
     // one (so that 0 stays below every expert). Keys order as (upper bits of

@@ -185,3 +185,31 @@ def test_near_ties_take_the_exact_selection(E, k):
         for n, e in enumerate(top):
             g[t, e] = vals[n % len(vals)]
     check_router(g, k)
+
+
+@pytest.mark.parametrize("E,k", [(64, 6), (128, 8), (256, 8), (64, 1)])
+def test_planted_ties_around_the_selection_boundary(E, k):
+    # Equal and 1-2 ulp apart logits planted at chosen ranks of each row:
+    # straddling the k-th / (k+1)-th boundary, inside the selected k (a run
+    # of three equal values; 1 and 2 ulps apart), and just outside it. Indices
+    # must stay bit-exact (ties to the lower expert), weights within 1e-6.
+    T = 3000
+    g = router_inputs(T, E, seed=211 + E + k)
+    up = lambda v: np.nextafter(np.float32(v), np.float32(np.inf))  # noqa: E731
+    dn = lambda v: np.nextafter(np.float32(v), np.float32(-np.inf))  # noqa: E731
+    for t in range(T):
+        row = g[t]
+        o = np.argsort(-row, kind="stable")
+        kind = t % 6
+        if kind == 0:    # ranks k-1 and k equal
+            row[o[k]] = row[o[k - 1]]
+        elif kind == 1:  # rank k one ulp above rank k-1's value
+            row[o[k]] = up(row[o[k - 1]])
+        elif kind == 2:  # ranks 0..2 equal
+            row[o[1]] = row[o[2]] = row[o[0]]
+        elif kind == 3:  # ranks 1, 2 one and two ulps below rank 0
+            row[o[1]] = dn(row[o[0]])
+            row[o[2]] = dn(row[o[1]])
+        elif kind == 4:  # ranks k .. k+2 equal
+            row[o[k + 1]] = row[o[k + 2]] = row[o[k]]
+    check_router(g, k)
