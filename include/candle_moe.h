@@ -44,6 +44,11 @@ enum {
  *   topk_weight          [num_tokens, topk] f32   (descending probability)
  *   topk_indices         [num_tokens, topk] u32   (ties -> lower expert index)
  *   token_expert_indices [num_tokens, topk] u32   (= j * num_tokens + t)
+ * Indices are those of the exact softmax (f64 exponential rounded to f32,
+ * f64 row sum, correctly rounded quotient), ties included. So are the
+ * weights, except for f32 weights with num_experts 64, 128 or 256 and
+ * topk < num_experts / 8: there they come from an f32 softmax within 6e-7
+ * relative of the exact one.
  * num_tokens is a C int, as the reference caller passes it (the reference
  * definition's int64_t parameter did not match its caller). On invalid
  * sizes nothing is launched and candle_moe_last_error() says why.
