@@ -143,6 +143,7 @@ struct Problem {
     bool rows_path;   // pair path: each pair's weighted down row stored, then summed per token (no atomics)
     int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
     int split_target; // K splits: the kernels aim at this many workgroups (live tiles * splits)
+    bool narrow2;     // pair-path down / fc2 GEMM on 128-column tiles of the 32-row kernel
 };
 
 // CUs per XCD of the current device (its CUs over the 8 XCDs of MI355X), 0
@@ -369,7 +370,20 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 &&
                   (double)P * H * 2.0 <= kRowsMaxBytes;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
-    p.n_tiles2 = cdiv(H, gemm_tile_cols(kDown, p.cfg));
+    // Decode down / fc2 GEMM (32-row kernel, 16-bit weights): 128-column
+    // tiles where the 256-column tiling would leave CUs without a tile (and
+    // so split K) and K = I is long. Twice the tiles then fill the device
+    // with fewer or no K splits, which saves the split-K fixup: Qwen3 T=8 /
+    // 16 / 64 18.5 -> 16.8, 24.0 -> 21.9, 25.0 -> 23.1 us, Nomic T=16 / 64
+    // 16.0 -> 13.6, 16.5 -> 14.2 us. With I = 768 (Qwen3-30B-A3B) or live
+    // tiles enough for every CU the wide tiles stay ahead (T=1: 13.1 against
+    // 13.6 us, T=16: 50.6 against 56.1 us).
+    const int down_cols = (p.cfg == kLdsRows32 && !fp8 && I >= 1536 &&
+                           touched * cdiv(H, 256) < 8LL * std::max(cus_per_xcd(), 32))
+                              ? 128
+                              : gemm_tile_cols(kDown, p.cfg);
+    p.narrow2 = down_cols == 128 && gemm_tile_cols(kDown, p.cfg) != 128;
+    p.n_tiles2 = cdiv(H, down_cols);
     p.split1 = p.split2 = 1;
     // tail balance for the 8-wave 256x256 kernel (its K splits meet in the
     // split-K fixup): the tiles of each XCD's last, partly filled round are
@@ -562,6 +576,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.a_bytes = p.P * p.I * (p.dtype == kF32 ? 4 : 2);
     const int mode2 = p.rows_path ? (qwen3 ? kDownRows : kFc2Rows) : (qwen3 ? kDown : kFc2);
     g2.n_tiles = p.n_tiles2;
+    g2.narrow = p.narrow2 ? 1 : 0;
     g2.ksplit = p.split2;
     g2.split_target = p.split_target;
     g2.partial = reinterpret_cast<float*>(ws + L.partial);

@@ -625,6 +625,13 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
                 break;
             case kLdsRows32:
+                if constexpr (MODE == kDown || MODE == kFc2) {
+                    if (a.narrow) {
+                        hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0,
+                                           stream, a);
+                        break;
+                    }
+                }
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0, stream, a);
                 break;
             // two workgroups per CU (72 KB of LDS, at most 256 VGPRs each): one
