@@ -143,6 +143,7 @@ struct Problem {
     bool rows_path;   // pair path: each pair's weighted down row stored, then summed per token (no atomics)
     int tail_cus;     // tail balance of the 8-wave 256x256 kernel: CUs per XCD (0 = off)
     int split_target; // K splits: the kernels aim at this many workgroups (live tiles * splits)
+    bool narrow1;     // fc1 GEMM on 128-column tiles of the 32-row kernel
     bool narrow2;     // pair-path down / fc2 GEMM on 128-column tiles of the 32-row kernel
 };
 
@@ -370,6 +371,14 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 &&
                   (double)P * H * 2.0 <= kRowsMaxBytes;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
+    // Decode fc1 (Nomic) likewise on 128-column tiles where the 256-column
+    // ones would split K: T=16 / 64 16.8 -> 13.4, 15.2 -> 12.9 us. (The
+    // gate/up tile cannot narrow the same way: a wave holds matching gate and
+    // up columns, so 128 columns leave two waves per workgroup, whose fewer
+    // loads in flight lost 2.6-3.5 us at Qwen3 T=16 / 64.)
+    const long long dev_wgs = 8LL * std::max(cus_per_xcd(), 32);
+    p.narrow1 = p.cfg == kLdsRows32 && !fp8 && p.moe_type == kNomic && touched * cdiv(I, 256) < dev_wgs;
+    if (p.narrow1) p.n_tiles1 = cdiv(I, 128);
     // Decode down / fc2 GEMM (32-row kernel, 16-bit weights): 128-column
     // tiles where the 256-column tiling would leave CUs without a tile (and
     // so split K) and K = I is long. Twice the tiles then fill the device
@@ -378,8 +387,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // 16.0 -> 13.6, 16.5 -> 14.2 us. With I = 768 (Qwen3-30B-A3B) or live
     // tiles enough for every CU the wide tiles stay ahead (T=1: 13.1 against
     // 13.6 us, T=16: 50.6 against 56.1 us).
-    const int down_cols = (p.cfg == kLdsRows32 && !fp8 && I >= 1536 &&
-                           touched * cdiv(H, 256) < 8LL * std::max(cus_per_xcd(), 32))
+    const int down_cols = (p.cfg == kLdsRows32 && !fp8 && I >= 1536 && touched * cdiv(H, 256) < dev_wgs)
                               ? 128
                               : gemm_tile_cols(kDown, p.cfg);
     p.narrow2 = down_cols == 128 && gemm_tile_cols(kDown, p.cfg) != 128;
@@ -496,6 +504,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.act = p.act;
     const int mode1 = qwen3 ? kGateUp : kFc1;
     g1.n_tiles = p.n_tiles1;
+    g1.narrow = p.narrow1 ? 1 : 0;
     g1.m_tiles_max = m_tiles_max;
     g1.ksplit = p.split1;
     g1.split_target = p.split_target;
@@ -544,6 +553,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.pair_dest = nullptr;
         g2.fold_w = 0;
         g2.ksplit = 1;
+        g2.narrow = 0;
         g2.zero_f32 = nullptr;
         g2.zero_n = 0;
         g2.overwrite = overwrite ? 1 : 0;

@@ -115,8 +115,8 @@ struct GemmArgs {
     // of B0 and (kGateUp) B1
     const float* scale0;
     const float* scale1;
-    // 32-row kernel, kDown / kFc2 with 16-bit weights: 128-column tiles
-    // instead of 256 (n_tiles counts those)
+    // 32-row kernel, kFc1 / kDown / kFc2 with 16-bit weights: 128-column
+    // tiles instead of 256 (n_tiles counts those)
     int narrow;
 };
 constexpr int kTailMaxSplit = 8;

@@ -564,7 +564,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         // which splits finish)
         // loads in flight per batch: the atomic-combine kernels keep their
         // row table in registers and have less room
-        constexpr int FIX_BATCH = ATOMIC ? 4 : 8;
+        constexpr int FIX_BATCH = (ATOMIC || MB * NB < 2) ? 4 : 8;
         if (nsplit > 1 &&
             !splitk_fixup<MB, NB, NW, FIX_BATCH, (BM <= 32)>(a, acc, fix_slot0, fix_ctr, ks, nsplit, wave, lane))
             return;
@@ -625,7 +625,7 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
                 hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
                 break;
             case kLdsRows32:
-                if constexpr (MODE == kDown || MODE == kFc2) {
+                if constexpr (MODE == kDown || MODE == kFc2 || MODE == kFc1) {
                     if (a.narrow) {
                         hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0,
                                            stream, a);
