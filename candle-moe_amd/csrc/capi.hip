@@ -492,6 +492,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.C = inter;
     g1.routing_w = rw;
     g1.sorted_pair = gb.sorted_pair;
+    g1.sorted_n = (int)p.P;
     g1.tile_row = gb.tile_row;
     g1.tile_exp = gb.tile_exp;
     g1.num_tiles = gb.num_tiles;

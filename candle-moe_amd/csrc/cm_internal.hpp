@@ -78,6 +78,7 @@ struct GemmArgs {
     void* C;                  // inter [P,N] (dtype) or f32 accumulator [T,N]
     const float* routing_w;   // [T*k]
     const int32_t* sorted_pair;
+    int sorted_n;             // entries of sorted_pair (P)
     const int32_t* tile_row;
     const int32_t* tile_exp;
     const int32_t* num_tiles;

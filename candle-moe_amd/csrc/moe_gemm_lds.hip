@@ -134,18 +134,20 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // ---- per-lane DMA offsets, fixed for the whole K loop (gathered row or
     // column chunk and the chunk's swizzled slot); the K position of a full
     // tile goes into the instruction's SGPR offset. A: instruction i of this
-    // wave covers rows RPA*q .. RPA*q+RPA-1, q = NW*i + wave. Lanes outside the
-    // operand carry kOob (the buffer returns zeros).
+    // wave covers rows RPA*q .. RPA*q+RPA-1, q = NW*i + wave. Rows past the
+    // group's end (r >= m_valid) are not masked: row i of a product depends
+    // on row i of A only and those rows are never stored, and every load
+    // stays in range (the sorted-pair index is clamped to the array; an A
+    // offset past a_bytes, or wrapped, reads zeros; offsets stay multiples of
+    // 16 bytes). So the first DMA waits for the tile table and the gather
+    // only, not for the group's end (offsets[grp + 1]), loaded alongside.
     uint32_t a_off[A_INS];
 #pragma unroll
     for (int i = 0; i < A_INS; ++i) {
         const int r = RPA * (NW * i + wave) + lane / ACH;
         const int kc = a_swz<ACH>(r, lane % ACH) * 8;  // k offset of the chunk that lands at this lane's slot
-        a_off[i] = kOob;
-        if (r < m_valid) {
-            const int src = GATHER ? a.sorted_pair[r0 + r] / a.k_top : r0 + r;
-            a_off[i] = ((uint32_t)src * (uint32_t)a_pitch + (uint32_t)kc) * 2u;
-        }
+        const int src = GATHER ? a.sorted_pair[min(r0 + r, a.sorted_n - 1)] / a.k_top : r0 + r;
+        a_off[i] = ((uint32_t)src * (uint32_t)a_pitch + (uint32_t)kc) * 2u;
     }
     // B [N,K]: like A over the column tile's rows n. B [K,N]: instruction i
     // (i % SUB_INS within sub-tile i / SUB_INS) covers k-rows RPI*q ..
