@@ -134,20 +134,27 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // ---- per-lane DMA offsets, fixed for the whole K loop (gathered row or
     // column chunk and the chunk's swizzled slot); the K position of a full
     // tile goes into the instruction's SGPR offset. A: instruction i of this
-    // wave covers rows RPA*q .. RPA*q+RPA-1, q = NW*i + wave. Rows past the
-    // group's end (r >= m_valid) are not masked: row i of a product depends
-    // on row i of A only and those rows are never stored, and every load
-    // stays in range (the sorted-pair index is clamped to the array; an A
-    // offset past a_bytes, or wrapped, reads zeros; offsets stay multiples of
-    // 16 bytes). So the first DMA waits for the tile table and the gather
-    // only, not for the group's end (offsets[grp + 1]), loaded alongside.
+    // wave covers rows RPA*q .. RPA*q+RPA-1, q = NW*i + wave. Gathered rows
+    // (gate/up, fc1) past the group's end (r >= m_valid) are not masked: row
+    // i of a product depends on row i of A only and those rows are never
+    // stored, and every load stays in range (the sorted-pair index is clamped
+    // to the array; an A offset past a_bytes, or wrapped, reads zeros;
+    // offsets stay multiples of 16 bytes), so the first DMA waits for the
+    // tile table and the gather only, not for the group's end (offsets[grp +
+    // 1]), loaded alongside. Contiguous rows (the other modes) need no gather
+    // and stay masked (kOob lanes fetch nothing), which saves their
+    // partly filled tiles the traffic of the rows past the group.
     uint32_t a_off[A_INS];
 #pragma unroll
     for (int i = 0; i < A_INS; ++i) {
         const int r = RPA * (NW * i + wave) + lane / ACH;
         const int kc = a_swz<ACH>(r, lane % ACH) * 8;  // k offset of the chunk that lands at this lane's slot
-        const int src = GATHER ? a.sorted_pair[min(r0 + r, a.sorted_n - 1)] / a.k_top : r0 + r;
-        a_off[i] = ((uint32_t)src * (uint32_t)a_pitch + (uint32_t)kc) * 2u;
+        if constexpr (GATHER) {
+            const int src = a.sorted_pair[min(r0 + r, a.sorted_n - 1)] / a.k_top;
+            a_off[i] = ((uint32_t)src * (uint32_t)a_pitch + (uint32_t)kc) * 2u;
+        } else {
+            a_off[i] = r < m_valid ? ((uint32_t)(r0 + r) * (uint32_t)a_pitch + (uint32_t)kc) * 2u : kOob;
+        }
     }
     // B [N,K]: like A over the column tile's rows n. B [K,N]: instruction i
     // (i % SUB_INS within sub-tile i / SUB_INS) covers k-rows RPI*q ..
