@@ -412,6 +412,15 @@ def set_combine_policy(policy: int) -> None:
     check(lib().candle_moe_set_combine_policy(int(policy)))
 
 
+# grouping launch modes of candle_moe_set_grouping_mode (include/candle_moe.h)
+GROUPING_AUTO, GROUPING_TWO_LAUNCHES, GROUPING_ONE_LAUNCH_RECOUNT = 0, 1, 2
+
+
+def set_grouping_mode(mode: int) -> None:
+    """Process-wide grouping launch mode of fused_moe (GROUPING_*; default auto)."""
+    check(lib().candle_moe_set_grouping_mode(int(mode)))
+
+
 # GEMM kernel codes of candle_moe_set_tile_policy (include/candle_moe.h)
 TILE_AUTO, TILE_128, TILE_LDS_128, TILE_W8, TILE_ROWS32, TILE_128x256_OCC2, TILE_F32_ROWS32, TILE_F32_128 = \
     0, 1, 5, 7, 12, 14, 15, 16

@@ -166,6 +166,7 @@ static int cus_per_xcd() {
 }
 
 struct Layout {
+    size_t sync;  // 4 ints of the one-launch grouping (offset 0, 256 bytes)
     size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles;
     size_t k_offsets, k_block_counts, tok_sorted, tile_row2, tile_key2, num_tiles2, pair_dest;
     size_t inter, acc, partial, counters, total;
@@ -184,6 +185,12 @@ constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
 static int g_combine_policy = 0;
 // 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
+// Grouping launches above kGroupSmallMax items: 0 one launch where the
+// workspace's counters are known to start at zero (library-owned
+// workspaces, the no-allocation scratch) and the launch fits the device,
+// else two; 1 always two; 2 one launch whose workgroups all take the recount
+// fallback (tests).
+static int g_grouping_mode = 0;
 
 static long long set_tiles_max(const Problem& p) {
     return (p.T + p.BM - 1) / p.BM + (p.nkeys < p.T ? p.nkeys : p.T);
@@ -198,6 +205,7 @@ static Layout make_layout(const Problem& p) {
     const long long nb = grouping_blocks(p.P);
     const long long mt = grouping_max_tiles(p.P, p.E, p.BM);
     size_t o = 0;
+    L.sync = o; o += 256;
     L.offsets = o; o += a256((size_t)(p.E + 2) * 4);
     L.block_counts = o; o += a256((size_t)(nb > 0 ? nb : 1) * p.E * 4);
     L.sorted_pair = o; o += a256((size_t)(p.P > 0 ? p.P : 1) * 4);
@@ -435,9 +443,12 @@ struct Fp8Weights {
     const float* down_scale;
 };
 
+// sync_zero: the workspace's grouping counters (Layout::sync) are zero
+// (library-owned workspaces: cleared at allocation, left zero by every
+// launch), which allows the one-launch grouping.
 static int run_moe(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
                    const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, hipStream_t s,
-                   const Fp8Weights* f8 = nullptr) {
+                   const Fp8Weights* f8 = nullptr, bool sync_zero = false) {
     auto gemm = [&](int mode, const GemmArgs& g) {
         return f8 ? launch_moe_gemm_w8(mode, p.dtype, g, s) : launch_moe_gemm(mode, p.dtype, p.cfg, g, s);
     };
@@ -481,7 +492,11 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         GroupJob tj = {};
         if (p.set_path) tj = set_grouping_job(idx, p.T, p.k, p.E, p.nkeys, p.BM, tb, pair_dest);
         ProfScope ps(kSlotGroup, s);
-        e = launch_groupings(pj, p.set_path ? &tj : nullptr, s);
+        const bool one = sync_zero && g_grouping_mode != 1;
+        const int cus = cus_per_xcd() > 0 ? 8 * cus_per_xcd() : 0;
+        e = launch_groupings(pj, p.set_path ? &tj : nullptr, s,
+                             one ? reinterpret_cast<int32_t*>(ws + L.sync) : nullptr, cus,
+                             g_grouping_mode == 2 ? -1 : kGroupSpin);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe grouping");
 
@@ -657,6 +672,13 @@ static OwnedWs* owned_ws_locked(int dev, hipStream_t s, size_t need, hipError_t&
     void* mem = nullptr;
     err = hipMallocAsync(&mem, want, s);
     if (err != hipSuccess) return nullptr;
+    // the one-launch grouping's counters start at zero (a kernel, not a
+    // memset node, should the call be captured into a graph)
+    err = launch_fill_zero_f32(reinterpret_cast<float*>(mem), 64, s);
+    if (err != hipSuccess) {
+        (void)hipFreeAsync(mem, s);
+        return nullptr;
+    }
     if (w) {
         if (w->ptr) (void)hipFreeAsync(w->ptr, s);
         w->ptr = mem;
@@ -715,7 +737,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
     if (!w) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s", L.total,
                              hipGetErrorString(e));
     return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                   out, overwrite, reinterpret_cast<char*>(w->ptr), s, f8);
+                   out, overwrite, reinterpret_cast<char*>(w->ptr), s, f8, true);
 }
 
 // ----------------------------------------------- fused MoE without allocation
@@ -773,7 +795,7 @@ int fused_moe_noalloc_impl(const void* x, const void* gate, const void* up, cons
     // every piece of the layout that must start at zero (split-K arrival
     // counters, the f32 accumulator) is cleared by this call's own kernels
     return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                   out, false, reinterpret_cast<char*>(ws), reinterpret_cast<hipStream_t>(stream));
+                   out, false, reinterpret_cast<char*>(ws), reinterpret_cast<hipStream_t>(stream), nullptr, true);
 }
 
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
@@ -993,6 +1015,12 @@ const char* candle_moe_last_error(void) { return cm::g_last_error.c_str(); }
 int candle_moe_set_combine_policy(int policy) {
     if (policy < 0 || policy > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "combine policy must be 0, 1 or 2");
     cm::g_combine_policy = policy;
+    return CANDLE_MOE_OK;
+}
+
+int candle_moe_set_grouping_mode(int mode) {
+    if (mode < 0 || mode > 2) return cm::set_error(CANDLE_MOE_ERR_INVALID, "grouping mode must be 0, 1 or 2");
+    cm::g_grouping_mode = mode;
     return CANDLE_MOE_OK;
 }
 

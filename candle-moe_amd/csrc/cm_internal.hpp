@@ -37,6 +37,9 @@ inline long long grouping_max_tiles(long long P, int E, int BM) { return (P + BM
 // ids sorted ascending (ids >= E become E and sort last), read as base-(E+1)
 // digits. b.sorted_pair receives the token of each sorted position,
 // pair_dest[t*k + j] = pos(t)*k + rank of slot j in the token's sorted set.
+// Polls (each s_sleep 2, ~128 clocks) a one-launch grouping workgroup makes
+// for the rest of its job before it recounts on its own (~2 ms).
+constexpr int kGroupSpin = 1 << 15;
 constexpr int kSetMaxK = 8;
 constexpr int kSetMaxKeys = 1024;
 
@@ -56,8 +59,12 @@ GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, i
                           int32_t* pair_dest);
 size_t a256_bytes(size_t x);  // x rounded up to 256 bytes
 // The pair grouping and optionally the token grouping: one launch when both
-// have at most kGroupSmallMax items, else two (histogram, scan + scatter).
-hipError_t launch_groupings(const GroupJob& pairs, const GroupJob* tokens, hipStream_t stream);
+// have at most kGroupSmallMax items, or when sync (4 ints, zero before the
+// first launch, left zero) is given and the launch has at most max_one
+// workgroups (one-launch grouping, spin: its wait bound); else two
+// (histogram, scan + scatter).
+hipError_t launch_groupings(const GroupJob& pairs, const GroupJob* tokens, hipStream_t stream,
+                            int32_t* sync = nullptr, int max_one = 0, int spin = 0);
 
 // ----------------------------------------------------------- grouped GEMM
 enum GemmMode : int {

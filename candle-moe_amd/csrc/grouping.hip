@@ -10,7 +10,9 @@
 // aliasing counts and offsets (/root/reference/kernels/preprocessing.cuh:296-298).
 //
 // Up to kGroupSmallMax items one workgroup does everything (small_body), one
-// launch. Beyond that, two launches, no host synchronisation:
+// launch. Beyond that, one launch where the workspace's counters are known
+// to start at zero (one_launch_body: the two phases below with a bounded
+// wait between them), else two launches, no host synchronisation:
 //   1. hist_body   : each workgroup histograms kGroupChunk items in LDS and
 //                    stores its per-bin counts
 //   2. scatter_body: each workgroup stages every block's counts in LDS (all
@@ -91,8 +93,10 @@ __device__ __forceinline__ int item_bin(const uint32_t* __restrict__ idx, long l
     return item_bin_of<TOK, K>(raw, E, rank);
 }
 
-// Histogram of block blk of job j into s_cnt ([4 waves][nbins] of LDS).
-template <bool TOK, int K>
+// Histogram of block blk of job j into s_cnt ([4 waves][nbins] of LDS),
+// stored to block_counts (COH: device-coherent stores, read by other
+// workgroups of the same launch).
+template <bool TOK, int K, bool COH = false>
 __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
     const uint32_t* __restrict__ idx = j.idx;
     const long long P = j.items;
@@ -117,9 +121,14 @@ __device__ void hist_body(const GroupJob& j, int blk, int32_t* s_cnt) {
     for (int s = 0; s < IPT; ++s)
         if (bin[s] >= 0) atomicAdd(mine + bin[s], 1);
     __syncthreads();
-    for (int e = threadIdx.x; e < nbins; e += kGroupThreads)
-        block_counts[(long long)blk * nbins + e] =
-            s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
+    for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+        const int32_t c = s_cnt[e] + s_cnt[nbins + e] + s_cnt[2 * nbins + e] + s_cnt[3 * nbins + e];
+        if constexpr (COH)
+            __hip_atomic_store(block_counts + (long long)blk * nbins + e, c, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        else
+            block_counts[(long long)blk * nbins + e] = c;
+    }
 }
 
 // Exclusive scans of u[0..n) and v[0..n) in place (one workgroup of
@@ -201,8 +210,13 @@ __device__ void block_exclusive_scan2(int32_t* u, int32_t* v, int n, int32_t* s_
 // every item goes to position + its rank.
 // LDS: [NW][nbins] per-wave counts, [nbins] totals, [nbins] tile counts,
 // [nbins] bases, [threads] scan scratch.
+// Where scatter_body takes the per-block counts from: the previous launch's
+// table, this launch's table (written by the other workgroups with
+// device-coherent stores before they counted themselves in), or a recount of
+// every item by this workgroup alone.
+enum CountSrc : int { kCountsPrevLaunch = 0, kCountsCoherent = 1, kCountsRecount = 2 };
 template <bool TOK, int K>
-__device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem) {
+__device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem, int src = kCountsPrevLaunch) {
     constexpr int NW = kGroupThreads / 64;
     constexpr int IPT = kGroupChunk / kGroupThreads;  // items per lane
     const uint32_t* __restrict__ idx = j.idx;
@@ -234,11 +248,39 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem) {
         const long long p = wbase + s * 64 + lane;
         if (p < P) item_load<TOK, K>(idx, p, raw[s]);
     }
+    if (src == kCountsRecount) {
+        // every block's histogram again, one block at a time (the fallback
+        // of the one-launch grouping; per-wave LDS counts in s_wc)
+        for (int e = threadIdx.x; e < nbins; e += kGroupThreads) s_tot[e] = s_base[e] = 0;
+        constexpr int HIPT = kGroupChunk / kGroupThreads;
+        int rk[K];
+        for (int b2 = 0; b2 < nblocks; ++b2) {
+            int hb[HIPT];
+#pragma unroll
+            for (int q = 0; q < HIPT; ++q) {
+                const long long p = (long long)b2 * kGroupChunk + q * kGroupThreads + threadIdx.x;
+                hb[q] = p < P ? item_bin<TOK, K>(idx, p, E, rk) : -1;
+            }
+            for (int i = threadIdx.x; i < NW * nbins; i += kGroupThreads) s_wc[i] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < HIPT; ++q)
+                if (hb[q] >= 0) atomicAdd(s_wc + wave * nbins + hb[q], 1);
+            __syncthreads();
+            for (int e = threadIdx.x; e < nbins; e += kGroupThreads) {
+                int32_t c = 0;
+                for (int w = 0; w < NW; ++w) c += s_wc[w * nbins + e];
+                s_tot[e] += c;
+                if (b2 < blk) s_base[e] += c;
+            }
+            __syncthreads();
+        }
+    }
     int G = 1;
     while (G < 64 && 2 * G * nbins <= kGroupThreads) G *= 2;
     const int gj = (int)threadIdx.x & (G - 1), ge = (int)threadIdx.x / G, estep = kGroupThreads / G;
     constexpr int U = 16;
-    for (int e0 = 0; e0 < nbins; e0 += estep) {
+    for (int e0 = 0; src != kCountsRecount && e0 < nbins; e0 += estep) {
         const int e = e0 + ge;
         int32_t tot = 0, bas = 0;
         for (int b0 = gj; b0 < nblocks; b0 += U * G) {
@@ -246,7 +288,12 @@ __device__ void scatter_body(const GroupJob& j, int blk, int32_t* s_mem) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int b2 = b0 + u * G;
-                c[u] = (e < nbins && b2 < nblocks) ? block_counts[b2 * nbins + e] : 0;
+                c[u] = 0;
+                if (e < nbins && b2 < nblocks)
+                    c[u] = src == kCountsCoherent
+                               ? __hip_atomic_load(block_counts + b2 * nbins + e, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : block_counts[b2 * nbins + e];
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -441,6 +488,57 @@ __device__ void small_body(const GroupJob& j, int32_t* s_mem) {
     }
 }
 
+// One-launch multi-workgroup grouping: histogram of this block's chunk,
+// stored device-coherently; the workgroup counts itself in at sync[0] and
+// waits (at most `spin` polls) until every block of the job has; then the
+// scatter as scatter_body, from the counts table. A workgroup whose wait runs
+// out (its job's workgroups not all resident, which the host's grid cap makes
+// the exception) recounts every item itself instead, so no wait is
+// unbounded; spin < 0 makes every workgroup recount (tests). Each workgroup
+// then counts itself out at sync[1]; the last one out resets both counters to
+// zero for the next launch (every workgroup has counted itself in and
+// finished waiting by then). sync must be zero before the first launch.
+template <bool TOK, int K>
+__device__ void one_launch_body(const GroupJob& j, int blk, int32_t* s_mem, int32_t* sync, int spin) {
+    __shared__ int s_ok;
+    hist_body<TOK, K, true>(j, blk, s_mem);
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this thread's count stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int ok = 0;
+        if (spin >= 0) {
+            for (int it = 0;; ++it) {
+                ok = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= j.nb;
+                if (ok || it >= spin) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    scatter_body<TOK, K>(j, blk, s_mem, s_ok ? kCountsCoherent : kCountsRecount);
+    if (threadIdx.x == 0) {
+        const int out = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (out == j.nb - 1) {
+            __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+template <int KB>
+__global__ __launch_bounds__(kGroupThreads) void grouping_one_k(GroupJob A, GroupJob B, int32_t* sync, int spin) {
+    extern __shared__ int32_t s_dyn[];
+    const int a_n = A.small ? 1 : A.nb;
+    if ((int)blockIdx.x < a_n) {
+        if (A.small) small_body<false, 1>(A, s_dyn);
+        else one_launch_body<false, 1>(A, blockIdx.x, s_dyn, sync, spin);
+    } else if constexpr (KB > 0) {
+        if (B.small) small_body<true, KB>(B, s_dyn);
+        else one_launch_body<true, KB>(B, blockIdx.x - a_n, s_dyn, sync + 2, spin);
+    }
+}
+
 // The launches serve the pair grouping (A) and, on the expert-set path, the
 // token grouping (B, KB ids per token) together: in each, the first
 // workgroups work on A and the rest on B. A job of at most kGroupSmallMax
@@ -495,10 +593,23 @@ GroupJob set_grouping_job(const uint32_t* idx, int T, int k, int E, int nkeys, i
 }
 
 template <int KB>
-static hipError_t launch_groupings_k(const GroupJob& A, const GroupJob& B, bool has_b, hipStream_t stream) {
+static hipError_t launch_groupings_k(const GroupJob& A, const GroupJob& B, bool has_b, hipStream_t stream,
+                                     int32_t* sync, int max_one, int spin) {
     auto ints = [](long long n) { return (size_t)n * sizeof(int32_t); };
     const bool a_multi = !A.small, b_multi = has_b && !B.small;
     const int nb_multi = (a_multi ? A.nb : 0) + (b_multi ? B.nb : 0);
+    if (sync && nb_multi > 0) {
+        const int grid = (A.small ? 1 : A.nb) + (has_b ? (B.small ? 1 : B.nb) : 0);
+        if (grid <= max_one) {
+            auto lds1 = [&](const GroupJob& j) {
+                return j.small ? 6LL * j.nbins + kGroupThreads : 7LL * j.nbins + kGroupThreads;
+            };
+            const long long lds = std::max(lds1(A), has_b ? lds1(B) : 0LL);
+            hipLaunchKernelGGL(grouping_one_k<KB>, dim3(grid), dim3(kGroupThreads), ints(lds), stream, A, B, sync,
+                               spin);
+            return hipGetLastError();
+        }
+    }
     if (nb_multi > 0) {
         const int bins = std::max(a_multi ? A.nbins : 0, b_multi ? B.nbins : 0);
         hipLaunchKernelGGL(grouping_hist_k<KB>, dim3(nb_multi), dim3(kGroupThreads), ints(4LL * bins), stream, A, B);
@@ -512,7 +623,8 @@ static hipError_t launch_groupings_k(const GroupJob& A, const GroupJob& B, bool 
     return hipGetLastError();
 }
 
-hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t stream) {
+hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t stream, int32_t* sync, int max_one,
+                            int spin) {
     if (B && (B->k < 1 || B->k > kSetMaxK || B->nbins > kSetMaxKeys)) return hipErrorInvalidValue;
     // the scatter workgroups index the per-block count table with 32-bit ints
     if ((long long)A.nb * A.nbins + 16LL * kGroupThreads >= 0x7fffffffLL ||
@@ -520,15 +632,15 @@ hipError_t launch_groupings(const GroupJob& A, const GroupJob* B, hipStream_t st
         return hipErrorInvalidValue;
     const GroupJob b = B ? *B : GroupJob{};
     switch (B ? B->k : 0) {
-        case 0: return launch_groupings_k<0>(A, b, false, stream);
-        case 1: return launch_groupings_k<1>(A, b, true, stream);
-        case 2: return launch_groupings_k<2>(A, b, true, stream);
-        case 3: return launch_groupings_k<3>(A, b, true, stream);
-        case 4: return launch_groupings_k<4>(A, b, true, stream);
-        case 5: return launch_groupings_k<5>(A, b, true, stream);
-        case 6: return launch_groupings_k<6>(A, b, true, stream);
-        case 7: return launch_groupings_k<7>(A, b, true, stream);
-        case 8: return launch_groupings_k<8>(A, b, true, stream);
+        case 0: return launch_groupings_k<0>(A, b, false, stream, sync, max_one, spin);
+        case 1: return launch_groupings_k<1>(A, b, true, stream, sync, max_one, spin);
+        case 2: return launch_groupings_k<2>(A, b, true, stream, sync, max_one, spin);
+        case 3: return launch_groupings_k<3>(A, b, true, stream, sync, max_one, spin);
+        case 4: return launch_groupings_k<4>(A, b, true, stream, sync, max_one, spin);
+        case 5: return launch_groupings_k<5>(A, b, true, stream, sync, max_one, spin);
+        case 6: return launch_groupings_k<6>(A, b, true, stream, sync, max_one, spin);
+        case 7: return launch_groupings_k<7>(A, b, true, stream, sync, max_one, spin);
+        case 8: return launch_groupings_k<8>(A, b, true, stream, sync, max_one, spin);
         default: return hipErrorInvalidValue;
     }
 }

@@ -173,6 +173,17 @@ int candle_moe_set_combine_policy(int policy);
  * multiple of 4 or an operand is not 16-byte aligned).
  * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
 int candle_moe_set_tile_policy(int policy);
+
+/* Grouping of fused_moe above 2048 items (process-wide; no counterpart in the
+ * reference, whose preprocessing is /root/reference/kernels/preprocessing.cuh:5-313):
+ * 0 = one launch (per-block histograms, a bounded wait for every block's
+ *     counts, stable scatter) on library-owned workspaces and the
+ *     no-allocation scratch, two launches on caller workspaces (default),
+ * 1 = always two launches (histogram; scan + scatter),
+ * 2 = one launch in which every workgroup recounts all items itself instead
+ *     of waiting (the fallback of a wait that runs out; for tests).
+ * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
+int candle_moe_set_grouping_mode(int mode);
 /* Which path fused_moe takes for these sizes under the current policies:
  * bits 0-1: 2 = expert-set MFMA path, 1 = pair MFMA path, 0 = SIMT path;
  * bits 2 and up: the GEMM kernel (policy code above); -1 = invalid sizes. */

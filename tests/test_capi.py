@@ -227,6 +227,16 @@ def test_tile_policy_accepts_only_shipped_kernels():
     cm.set_tile_policy(0)
 
 
+def test_grouping_mode_setter():
+    for mode in (cm.GROUPING_TWO_LAUNCHES, cm.GROUPING_ONE_LAUNCH_RECOUNT, cm.GROUPING_AUTO):
+        cm.set_grouping_mode(mode)
+    for mode in (3, -1):
+        with pytest.raises(cm.CandleMoeError) as e:
+            cm.set_grouping_mode(mode)
+        assert e.value.code == cm.CANDLE_MOE_ERR_INVALID
+    cm.set_grouping_mode(cm.GROUPING_AUTO)
+
+
 def test_workspace_size():
     L = cm.lib()
     small = L.candle_moe_fused_moe_workspace_size(32, 64, 256, 8, 2, 1)

@@ -328,6 +328,42 @@ def test_multi_block_grouping_skewed_dropped_repeated():
         assert_close(got, want, RTOL[O.BF16], "combine %d" % combine)
 
 
+@pytest.mark.parametrize("T,H,I,E,k,mt,dt,skew", [
+    (9000, 64, 64, 8, 2, O.QWEN3, O.BF16, True),      # expert sets: pair and token groupings, 9 + 18 blocks
+    (3000, 128, 64, 16, 4, O.NOMIC, O.F16, False),   # pair path, 12 blocks
+    (700, 64, 64, 128, 8, O.QWEN3, O.BF16, False),   # 128 bins, 6 blocks
+])
+def test_grouping_launch_modes_agree(T, H, I, E, k, mt, dt, skew):
+    # one launch (a wait for every block's counts), two launches, and one
+    # launch whose workgroups all recount every item: the grouping is stable,
+    # so the three give the same sorted order and bit-identical outputs, also
+    # through the raw symbol (library workspace) and a caller workspace (two
+    # launches); checked against the oracle once
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, 41, mt)
+    if skew:
+        ri = ri.copy()
+        ri[::2, 0] = 3
+        ri[::13, 1] = 50
+        ri[5::17, 1] = ri[5::17, 0]
+    D = D if mt == O.QWEN3 else None
+    outs = {}
+    try:
+        for mode in (candle_moe.GROUPING_AUTO, candle_moe.GROUPING_TWO_LAUNCHES, candle_moe.GROUPING_ONE_LAUNCH_RECOUNT,
+                     candle_moe.GROUPING_AUTO):
+            candle_moe.set_grouping_mode(mode)
+            outs[mode] = (run_moe(x, G, U, D, rw, ri, E, k, O.SILU, mt, dt),
+                          run_raw(x, G, U, D, rw, ri, E, k, O.SILU, mt, dt),
+                          run_raw(x, G, U, D, rw, ri, E, k, O.SILU, mt, dt, workspace=True))
+    finally:
+        candle_moe.set_grouping_mode(candle_moe.GROUPING_AUTO)
+    ref = outs[candle_moe.GROUPING_TWO_LAUNCHES][0]
+    for mode, got in outs.items():
+        for g in got:
+            assert np.array_equal(g, ref), "grouping mode %d differs" % mode
+    want = O.fused_moe(x, G, U, D, rw, ri, E=E, k=k, act=O.SILU, moe_type=mt, dtype=dt, mode=O.MODE_F32ACC)
+    assert_close(ref, want, RTOL[dt], "grouping modes")
+
+
 def test_headline_shape_takes_expert_set_path():
     assert candle_moe.fused_moe_path(32768, 4096, 1536, 8, 2, O.BF16) == "expert-set"
     assert candle_moe.fused_moe_path(4096, 2048, 768, 128, 8, O.BF16) == "pairs"
