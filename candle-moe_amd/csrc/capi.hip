@@ -254,8 +254,8 @@ static Layout make_layout(const Problem& p) {
 // runs). out16: so does the output (the expert-set down GEMM stores straight
 // into it, 8 bytes at a time; otherwise the pair path, whose last pass
 // handles any alignment).
-// fp8: fp8 weights (candle_moe_fused_moe_fp8): the 32-row kernel for every
-// batch, on the pair path.
+// fp8: fp8 weights (candle_moe_fused_moe_fp8): the 32-row kernel for decode
+// batches, the 8-wave 256x256 kernel beyond, on the pair path.
 static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
                          Problem& p, bool aligned16 = true, bool out16 = true, bool fp8 = false) {
     if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
@@ -307,7 +307,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             return set_error(CANDLE_MOE_ERR_UNSUPPORTED,
                              "fused_moe_fp8: needs f16 or bf16 activations, hidden_dim and intermediate_dim multiples "
                              "of 16 and 16-byte aligned tensors (got dtype %u, %d, %d)", dtype, H, I);
-        p.cfg = kLdsRows32;
+        // the 32-row kernel streams each touched expert's weights once per
+        // row tile: decode batches; beyond, the 8-wave 256x256 kernel
+        p.cfg = (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
     } else if (p.mfma && !g_tile_policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
@@ -450,7 +452,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
                    const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, hipStream_t s,
                    const Fp8Weights* f8 = nullptr, bool sync_zero = false) {
     auto gemm = [&](int mode, const GemmArgs& g) {
-        return f8 ? launch_moe_gemm_w8(mode, p.dtype, g, s) : launch_moe_gemm(mode, p.dtype, p.cfg, g, s);
+        return f8 ? launch_moe_gemm_w8(mode, p.dtype, p.cfg, g, s) : launch_moe_gemm(mode, p.dtype, p.cfg, g, s);
     };
     const Layout L = make_layout(p);
     GroupingBufs gb = {};

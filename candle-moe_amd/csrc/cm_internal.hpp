@@ -189,7 +189,8 @@ hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, 
 // = K, strideB = N*K) with per-output-column scales (scale0 / scale1), on the
 // 32-row kernel (tile_rows(kLdsRows32)); 16-bit activations; modes kGateUp,
 // kFc1, kDown, kFc2.
-hipError_t launch_moe_gemm_w8(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
+// cfg: kLdsRows32 (decode) or kLds256w8
+hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
 

@@ -459,10 +459,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, f32x16 (&acc)[M
 // 32 rows of a write and the chunks of a row read land in distinct banks);
 // (2) the waves store whole rows, 16 bytes per lane, CPR lanes per row.
 // dst_rows[r]: output row of tile row r; rows >= m_valid are not stored.
-template <int DT, int MODE, int BM, int BN, int WM, int WN, int MB, int NB, int NW>
+// SC (fp8 weights): the f32 sums are first scaled by the tile's column
+// scales sc0 (gate/up: gate's, sc1 up's), indexed by the output column in
+// the tile.
+template <int DT, int MODE, int BM, int BN, int WM, int WN, int MB, int NB, int NW, bool SC = false>
 __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, f32x16 (&acc)[MB][NB], char* tile_lds,
                                                 const int32_t* dst_rows, int m_valid, int nt, int wm, int wn,
-                                                int lane, const float* pre_w) {
+                                                int lane, const float* pre_w, const float* sc0 = nullptr,
+                                                const float* sc1 = nullptr) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
     constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
@@ -496,10 +500,17 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, f32x16 (&acc)
                         float h[4];
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
+                            float gv = DUAL ? acc[mb][2 * q][4 * g + j] : acc[mb][q][4 * g + j];
+                            float uv = DUAL ? acc[mb][2 * q + 1][4 * g + j] : 1.0f;
+                            if constexpr (SC) {
+                                const int lc = lbase + 8 * g + nsub + j;  // output column in the tile
+                                gv *= sc0[lc];
+                                if constexpr (DUAL) uv *= sc1[lc];
+                            }
                             if constexpr (DUAL)
-                                h[j] = act_t<ACT>(acc[mb][2 * q][4 * g + j]) * acc[mb][2 * q + 1][4 * g + j];
+                                h[j] = act_t<ACT>(gv) * uv;
                             else
-                                h[j] = act_t<ACT>(acc[mb][q][4 * g + j]);
+                                h[j] = act_t<ACT>(gv);
                             h[j] *= ws;
                         }
                         put(ml, lbase + 8 * g + nsub, h[0], h[1], h[2], h[3]);
@@ -517,8 +528,16 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, f32x16 (&acc)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int i = 4 * g;
-                    put(ml, wn * WN + nb * 32 + 8 * g + nsub, ws * acc[mb][nb][i], ws * acc[mb][nb][i + 1],
-                        ws * acc[mb][nb][i + 2], ws * acc[mb][nb][i + 3]);
+                    const int lc = wn * WN + nb * 32 + 8 * g + nsub;
+                    float c0 = ws, c1 = ws, c2 = ws, c3 = ws;
+                    if constexpr (SC) {
+                        c0 *= sc0[lc];
+                        c1 *= sc0[lc + 1];
+                        c2 *= sc0[lc + 2];
+                        c3 *= sc0[lc + 3];
+                    }
+                    put(ml, lc, c0 * acc[mb][nb][i], c1 * acc[mb][nb][i + 1], c2 * acc[mb][nb][i + 2],
+                        c3 * acc[mb][nb][i + 3]);
                 }
             }
         }

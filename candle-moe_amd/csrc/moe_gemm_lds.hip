@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     __shared__ float s_w[ATOMIC ? BM : 1];
     __shared__ float s_sc[W8 ? BN : 1];
     // staged (row-contiguous) epilogue of the large tiles, see staged_epilogue
-    constexpr bool STAGED = SWAP && !W8 && BM >= 128;
+    constexpr bool STAGED = SWAP && BM >= 128;
     static_assert(!STAGED || NST * STAGE >= BM * (DUAL ? BN / 2 : BN) * 2, "output tile fits the stages");
     __shared__ int32_t s_dst[STAGED ? BM : 1];
 
@@ -189,10 +189,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // epilogue after the K loop
     float sc_pre = 1.0f;
     if constexpr (W8) {
-        static_assert(BN == 64 * NW, "one scale per thread");
+        static_assert(BN <= 64 * NW, "one scale per thread");
         const int c = DUAL ? nt * SUBN + tid % SUBN : nt * BN + tid;
         const float* src = (DUAL && tid >= SUBN) ? a.scale1 : a.scale0;
-        if (c < N) sc_pre = src[(long long)grp * N + c];
+        if (tid < BN && c < N) sc_pre = src[(long long)grp * N + c];
     }
 
     // Weight buffer resources of the current expert; on the expert-set path
@@ -559,7 +559,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         wait_lgkm0();
         block_barrier();
         const int ahead = kt + NST - 1;
-        const bool late = NW == 8 && wm == 1;  // row group 1 issues after its first k16 step
+        // row group 1 issues after its first k16 step (not with fp8 weights,
+        // whose compute_w8 has no DMA slot)
+        const bool late = NW == 8 && !W8 && wm == 1;
         if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
         if constexpr (W8) compute_w8(kt % NST);
         else compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
@@ -582,7 +584,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     const float* sc0 = nullptr;
     const float* sc1 = nullptr;
     if constexpr (W8) {
-        s_sc[tid] = sc_pre;
+        if (tid < BN) s_sc[tid] = sc_pre;
         __syncthreads();
         sc0 = s_sc;
         if constexpr (DUAL) sc1 = s_sc + SUBN;
@@ -598,8 +600,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                 }
             }
             __syncthreads();  // every wave is done with the stages
-            staged_epilogue<DT, MODE, BM, BN, WM, WN, MB, NB, NW>(a, acc, smem, SET ? s_tok : s_dst, m_valid, nt, wm,
-                                                                 wn, lane, pre_w);
+            staged_epilogue<DT, MODE, BM, BN, WM, WN, MB, NB, NW, W8>(a, acc, smem, SET ? s_tok : s_dst, m_valid, nt,
+                                                                     wm, wn, lane, pre_w, sc0, sc1);
             return;
         }
         if constexpr (SET && BN == 256 && NST * STAGE >= BM * (BN / 2) * 4) {
@@ -656,10 +658,24 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// fp8-weight GEMMs: the 32-row kernel (decode), pair-path modes only
+// fp8-weight GEMMs, pair-path modes only: the 32-row kernel (decode) or the
+// 8-wave 256x256 kernel with 3 LDS stages (48 KB each: the fp8 B tile is half
+// the 16-bit one) for larger batches
 template <int DT, int MODE>
-static hipError_t launch_w8_mode(const GemmArgs& a, hipStream_t stream) {
+static hipError_t launch_w8_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     const long long tiles = (long long)a.m_tiles_max * a.n_tiles;
+    if (cfg == kLds256w8) {
+        if constexpr (MODE == kGateUp || MODE == kFc1 || MODE == kDownRows) {
+            const long long nwg = a.tail_cus > 0 ? 8 * ((tiles + 7) / 8 + a.tail_cus) : tiles;
+            if (nwg > 0x7fffffffLL) return hipErrorInvalidValue;
+            if (nwg <= 0) return hipSuccess;
+            hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 3, 8, MODE, 2, 1, true>), dim3((int)nwg), dim3(512), 0,
+                               stream, a);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
+    if (cfg != kLdsRows32) return hipErrorInvalidValue;
     const long long nwg_l = split_grid(tiles, a);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     if (nwg_l <= 0) return hipSuccess;
@@ -674,18 +690,21 @@ static hipError_t launch_w8_mode(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 template <int DT>
-static hipError_t launch_w8_dt(int mode, const GemmArgs& a, hipStream_t stream) {
+static hipError_t launch_w8_dt(int mode, int cfg, const GemmArgs& a, hipStream_t stream) {
+    // [N,K] fp8 weights for every GEMM: fc2 (Nomic) runs the down kernels
     switch (mode) {
-        case kGateUp: return launch_w8_mode<DT, kGateUp>(a, stream);
-        case kFc1: return launch_w8_mode<DT, kFc1>(a, stream);
-        case kDown: return launch_w8_mode<DT, kDown>(a, stream);
-        case kFc2: return launch_w8_mode<DT, kDown>(a, stream);  // [N,K] fp8 weights: the same kernel
+        case kGateUp: return launch_w8_mode<DT, kGateUp>(cfg, a, stream);
+        case kFc1: return launch_w8_mode<DT, kFc1>(cfg, a, stream);
+        case kDown: return launch_w8_mode<DT, kDown>(cfg, a, stream);
+        case kFc2: return launch_w8_mode<DT, kDown>(cfg, a, stream);
+        case kDownRows: return launch_w8_mode<DT, kDownRows>(cfg, a, stream);
+        case kFc2Rows: return launch_w8_mode<DT, kDownRows>(cfg, a, stream);
         default: return hipErrorInvalidValue;
     }
 }
-hipError_t launch_moe_gemm_w8(int mode, int dtype, const GemmArgs& a, hipStream_t stream) {
-    if (dtype == kBF16) return launch_w8_dt<kBF16>(mode, a, stream);
-    if (dtype == kF16) return launch_w8_dt<kF16>(mode, a, stream);
+hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
+    if (dtype == kBF16) return launch_w8_dt<kBF16>(mode, cfg, a, stream);
+    if (dtype == kF16) return launch_w8_dt<kF16>(mode, cfg, a, stream);
     return hipErrorInvalidValue;
 }
 

@@ -162,9 +162,23 @@ def test_fused_moe_fp8_drops_out_of_range_experts():
     assert_close(got, want, RTOL[O.BF16], "fp8 with dropped pairs")
 
 
+@pytest.mark.parametrize("mt,T,H,I,act,dt", [
+    (O.QWEN3, 600, 256, 192, O.SILU, O.BF16),
+    (O.NOMIC, 700, 320, 256, O.GELU, O.F16),
+    (O.QWEN3, 333, 208, 272, O.RELU, O.F16),   # sizes off the 64-element tiles
+])
+def test_fused_moe_fp8_prefill_kernel_all_rows(mt, T, H, I, act, dt):
+    # beyond 32 pairs per touched expert the fp8 path runs the 8-wave 256x256
+    # kernel (gate/up or fc1, then the pair-row down / fc2 and the row sums)
+    E, k = 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, 0.0, seed=95 + T)
+    got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
+    assert_close(got, want, RTOL[dt], "fp8 prefill kernel vs f64 oracle on the dequantized weights")
+
+
 def test_fused_moe_fp8_prefill_batch_sampled_rows():
-    # the fp8 entry point runs the 32-row kernel at every batch size: 2048
-    # tokens give ~128 row tiles per GEMM and no K splits
+    # 2048 tokens: the 8-wave 256x256 fp8 kernel with the tail's K splits
     T, H, I, E, k = 2048, 1024, 512, 8, 2
     x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=92)
     got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16)
