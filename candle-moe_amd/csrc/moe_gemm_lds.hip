@@ -409,6 +409,56 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             mfma_step(af[kk], bfr);
         }
     };
+    // fp8 weights on the 8-wave kernel: the 16-bit loop's schedule (two
+    // register sets, one LDS read per MFMA); each B block is read as the
+    // lane's 8 raw code bytes (one ds_read_b64, half the 16-bit block's bytes)
+    // and converted right before its step's MFMAs
+    auto load_w8 = [&](const char* sA, const char* sB, int kk, u32x4 (&af)[MB], u32x2 (&br)[NB]) {
+        const int c = kk * 2 + lh;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int r = a_frag_row[mb];
+            af[mb] = *reinterpret_cast<const u32x4*>(sA + r * AROW + a_swz<ACH>(r, c) * 16);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int sub = DUAL ? (nb & 1) : 0;
+            const int r = DUAL ? wn * (WN / 2) + (nb >> 1) * 32 + lr : wn * WN + nb * 32 + lr;
+            br[nb] = *reinterpret_cast<const u32x2*>(sB + sub * W8_SUB_BYTES + r * KROW + a_swz<KCH>(r, kk) * 16 +
+                                                     lh * 8);
+        }
+    };
+    auto compute_w8i = [&](int stage) {
+        if (!rows_live) return;
+        const char* sA = smem + stage * STAGE;
+        const char* sB = sA + A_BYTES;
+        u32x4 af0[MB], af1[MB], bfr[NB];
+        u32x2 br0[NB], br1[NB];
+        auto cvt = [&](const u32x2 (&br)[NB]) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) bfr[nb] = fp8x8_to<DT>(br[nb]);  // exact in DT
+        };
+        load_w8(sA, sB, 0, af0, br0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w8(sA, sB, 1, af1, br1);
+        cvt(br0);
+        mfma_step(af0, bfr);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        load_w8(sA, sB, 2, af0, br0);
+        cvt(br1);
+        mfma_step(af1, bfr);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        load_w8(sA, sB, 3, af1, br1);
+        cvt(br0);
+        mfma_step(af0, bfr);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        cvt(br1);
+        mfma_step(af1, bfr);
+        __builtin_amdgcn_sched_barrier(0);
+    };
     auto compute = [&](int stage, int ds, int dk) {
         if (!rows_live) {
 #pragma unroll
@@ -563,7 +613,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         // whose compute_w8 has no DMA slot)
         const bool late = NW == 8 && !W8 && wm == 1;
         if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
-        if constexpr (W8) compute_w8(kt % NST);
+        if constexpr (W8 && NW == 8 && KSTEPS == 4) compute_w8i(kt % NST);
+        else if constexpr (W8) compute_w8(kt % NST);
         else compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
     }
     }
