@@ -336,7 +336,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // 404 us at T=12288).
     p.set_path = false;
     p.nkeys = 0;
-    if (p.mfma && !fp8 && out16 && (I % 64) == 0 && k <= kSetMaxK && g_combine_policy != 1) {
+    // (fp8 weights: on the 8-wave prefill kernel, whose expert-set GEMM keeps
+    // its accumulators in per-segment column units)
+    if (p.mfma && (!fp8 || p.cfg == kLds256w8) && out16 && (I % 64) == 0 && k <= kSetMaxK &&
+        g_combine_policy != 1) {
         long long nk = 1;
         for (int j = 0; j < k && nk <= kSetMaxKeys; ++j) nk *= (E + 1);
         if (nk <= kSetMaxKeys) {
@@ -575,12 +578,17 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.zero_f32 = nullptr;
         g2.zero_n = 0;
         g2.overwrite = overwrite ? 1 : 0;
+        if (f8) {  // codes [E][H][I] (down, or Nomic's fc2 in up): n-rows of I bytes, scales per expert
+            g2.ldb = p.I;
+            g2.scale0 = qwen3 ? f8->down_scale : f8->up_scale;
+            g2.scale1 = nullptr;
+        }
         const int mode2 = qwen3 ? kDownSet : kFc2Set;
         g2.n_tiles = cdiv(p.H, gemm_tile_cols(mode2, p.cfg));
         g2.m_tiles_max = (int)set_tiles_max(p);
         {
             ProfScope ps(kSlotGemm2, s);
-            e = launch_moe_gemm(mode2, p.dtype, p.cfg, g2, s);
+            e = gemm(mode2, g2);
         }
         if (e != hipSuccess) return hip_fail(e, "fused_moe down GEMM (expert sets)");
         return CANDLE_MOE_OK;

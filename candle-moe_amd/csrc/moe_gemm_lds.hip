@@ -85,6 +85,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     __shared__ int32_t s_tok[(ATOMIC || SET) ? BM : 1];
     __shared__ float s_w[ATOMIC ? BM : 1];
     __shared__ float s_sc[W8 ? BN : 1];
+    // fp8 expert sets: unit u_j[col] of segment j's column (its expert's
+    // column scale, or 1 for an all-zero column), [kSetMaxK][BN]
+    constexpr bool W8SET = W8 && SET;
+    __shared__ __attribute__((aligned(16))) float s_unit[W8SET ? kSetMaxK * BN : 4];
     // staged (row-contiguous) epilogue of the large tiles, see staged_epilogue
     constexpr bool STAGED = SWAP && BM >= 128;
     static_assert(!STAGED || NST * STAGE >= BM * (DUAL ? BN / 2 : BN) * 2, "output tile fits the stages");
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // columns: gate then up for kGateUp), loaded now, staged in LDS for the
     // epilogue after the K loop
     float sc_pre = 1.0f;
-    if constexpr (W8) {
+    if constexpr (W8 && !SET) {
         static_assert(BN <= 64 * NW, "one scale per thread");
         const int c = DUAL ? nt * SUBN + tid % SUBN : nt * BN + tid;
         const float* src = (DUAL && tid >= SUBN) ? a.scale1 : a.scale0;
@@ -338,6 +342,32 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                 if constexpr (SWAP) acc[mb][nb] = mfma32<DT>(bfr[nb], af[mb], acc[mb][nb]);
                 else acc[mb][nb] = mfma32<DT>(af[mb], bfr[nb], acc[mb][nb]);
             }
+    };
+    // fp8 expert sets: per-column unit changes of the accumulators. Lane l
+    // holds, for block nb and register group g, columns wn*WN + nb*32 + 8g +
+    // 4(l/32) .. +3 (the swapped MFMA layout), the same for every mb.
+    auto scale_acc = [&](auto&& factor4) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int col = wn * WN + nb * 32 + 8 * g + 4 * lh;
+                const f32x4 f = factor4(col);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) acc[mb][nb][4 * g + jj] *= f[jj];
+            }
+    };
+    auto rescale_units = [&](int j) {
+        scale_acc([&](int col) {
+            const f32x4 up = *reinterpret_cast<const f32x4*>(s_unit + (j - 1) * BN + col);
+            const f32x4 un = *reinterpret_cast<const f32x4*>(s_unit + j * BN + col);
+            return f32x4{up[0] / un[0], up[1] / un[1], up[2] / un[2], up[3] / un[3]};
+        });
+    };
+    auto to_absolute = [&](int j) {
+        scale_acc([&](int col) { return *reinterpret_cast<const f32x4*>(s_unit + j * BN + col); });
     };
     // LDS read instructions per k16 step (ds_read_b128 for A and [N,K] B,
     // two ds_read_b64_tr_b16 per [K,N] B block).
@@ -501,6 +531,16 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     }
     // expert-set down / fc2: the output row (token) of every tile row, staged
     // in LDS now (no registers to spare) for the epilogue
+    if constexpr (W8SET) {
+        // loaded next to s_tok's rows, whose wait the DMA waits for anyway
+        if (tid < BN) {
+            const int c = nt * BN + tid;
+            for (int j = 0; j < n_seg; ++j) {
+                const float sj = c < N ? a.scale0[(long long)seg_exp[j] * N + c] : 0.0f;
+                s_unit[j * BN + tid] = sj > 0.0f ? sj : 1.0f;
+            }
+        }
+    }
     if constexpr (SET) {
         if (tid < BM) s_tok[tid] = a.tok_sorted[r0 + (tid < m_valid ? tid : 0)];
     }
@@ -613,12 +653,24 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         // whose compute_w8 has no DMA slot)
         const bool late = NW == 8 && !W8 && wm == 1;
         if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
+        if constexpr (W8SET) {
+            // fp8 expert sets: the accumulators hold the current segment's
+            // column units; entering segment j they are rescaled by
+            // u_{j-1} / u_j (the K tiles of a segment never straddle one:
+            // seg_len is a multiple of BK)
+            const int kg = (kt0 + kt) * BK;
+            if (kt > 0 && rows_live && kg % a.seg_len == 0) rescale_units(kg / a.seg_len);
+        }
         if constexpr (W8 && NW == 8 && KSTEPS == 4) compute_w8i(kt % NST);
         else if constexpr (W8) compute_w8(kt % NST);
         else compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
     }
     }
 
+    if constexpr (W8SET) {
+        // to absolute values: the unit of the segment of this split's last K tile
+        if (rows_live && nk > 0) to_absolute(((kt0 + nk - 1) * BK) / a.seg_len);
+    }
     if constexpr (FIXUP) {
         // split K: the last split to finish a tile sums all partials in split
         // order and alone runs the epilogue (one atomic per output element and
@@ -634,7 +686,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // fp8 weights: the tile's column scales, staged in LDS
     const float* sc0 = nullptr;
     const float* sc1 = nullptr;
-    if constexpr (W8) {
+    if constexpr (W8 && !SET) {
         if (tid < BN) s_sc[tid] = sc_pre;
         __syncthreads();
         sc0 = s_sc;
@@ -651,8 +703,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                 }
             }
             __syncthreads();  // every wave is done with the stages
-            staged_epilogue<DT, MODE, BM, BN, WM, WN, MB, NB, NW, W8>(a, acc, smem, SET ? s_tok : s_dst, m_valid, nt,
-                                                                     wm, wn, lane, pre_w, sc0, sc1);
+            staged_epilogue<DT, MODE, BM, BN, WM, WN, MB, NB, NW, W8 && !SET>(a, acc, smem, SET ? s_tok : s_dst,
+                                                                             m_valid, nt, wm, wn, lane, pre_w, sc0,
+                                                                             sc1);
             return;
         }
         if constexpr (SET && BN == 256 && NST * STAGE >= BM * (BN / 2) * 4) {
@@ -716,7 +769,7 @@ template <int DT, int MODE>
 static hipError_t launch_w8_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     const long long tiles = (long long)a.m_tiles_max * a.n_tiles;
     if (cfg == kLds256w8) {
-        if constexpr (MODE == kGateUp || MODE == kFc1 || MODE == kDownRows) {
+        if constexpr (MODE == kGateUp || MODE == kFc1 || MODE == kDownRows || MODE == kDownSet) {
             const long long nwg = a.tail_cus > 0 ? 8 * ((tiles + 7) / 8 + a.tail_cus) : tiles;
             if (nwg > 0x7fffffffLL) return hipErrorInvalidValue;
             if (nwg <= 0) return hipSuccess;
@@ -750,6 +803,8 @@ static hipError_t launch_w8_dt(int mode, int cfg, const GemmArgs& a, hipStream_t
         case kFc2: return launch_w8_mode<DT, kDown>(cfg, a, stream);
         case kDownRows: return launch_w8_mode<DT, kDownRows>(cfg, a, stream);
         case kFc2Rows: return launch_w8_mode<DT, kDownRows>(cfg, a, stream);
+        case kDownSet: return launch_w8_mode<DT, kDownSet>(cfg, a, stream);
+        case kFc2Set: return launch_w8_mode<DT, kDownSet>(cfg, a, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -177,6 +177,51 @@ def test_fused_moe_fp8_prefill_kernel_all_rows(mt, T, H, I, act, dt):
     assert_close(got, want, RTOL[dt], "fp8 prefill kernel vs f64 oracle on the dequantized weights")
 
 
+@pytest.mark.parametrize("mt,T,H,I,E,k,act,dt,zero_cols,accumulate", [
+    (O.QWEN3, 600, 256, 192, 8, 2, O.SILU, O.BF16, False, False),
+    (O.QWEN3, 600, 256, 1536, 8, 2, O.SILU, O.BF16, True, False),    # 48 K tiles: tail K splits across segments
+    (O.QWEN3, 1500, 256, 1536, 8, 2, O.SILU, O.F16, False, True),
+    (O.QWEN3, 900, 256, 192, 6, 3, O.RELU, O.BF16, True, False),    # three segments per set
+    (O.NOMIC, 700, 320, 256, 8, 2, O.GELU, O.F16, True, True),
+])
+def test_fused_moe_fp8_expert_sets(mt, T, H, I, E, k, act, dt, zero_cols, accumulate):
+    # the expert-set down / fc2 GEMM with fp8 weights keeps its accumulators
+    # in the current segment's column units (rescaled at each segment start,
+    # made absolute after the K loop); all-zero weight columns (scale 0, unit
+    # 1) and accumulate mode included
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, 120 + T, mt)
+    if zero_cols:
+        if mt == O.QWEN3:
+            D = D.copy()
+            D[1, :, 5] = 0
+            D[E - 1, :, 7:9] = 0
+        else:
+            U = U.copy()
+            U[2, 3, :] = 0   # Nomic fc2 is [E,H,I]: output column 3 of expert 2
+    dev, deq = {}, {}
+    specs = [("g", G, True), ("u", U, mt == O.QWEN3)] + ([("d", D, True)] if mt == O.QWEN3 else [])
+    for name, w, kn in specs:
+        q, sc = candle_moe.quantize_fp8(to_dev(w, dt), input_kn=kn)
+        dev[name] = (q, sc)
+        d = O.dequantize_fp8(_np(q), _np(sc))
+        deq[name] = np.ascontiguousarray(np.transpose(d, (0, 2, 1))) if kn else d
+    init = O.to_dtype(O.randn((T, H), seed=121, std=0.5), dt) if accumulate else None
+    try:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_EXPERT_SETS)
+        got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt, out_init=init)
+    finally:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt, out_init=init)
+    assert_close(got, want, RTOL[dt], "fp8 expert sets vs f64 oracle on the dequantized weights")
+    # and the pair path on the same inputs
+    try:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_PAIRS)
+        got2 = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt, out_init=init)
+    finally:
+        candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+    assert_close(got2, want, RTOL[dt], "fp8 pair path vs f64 oracle")
+
+
 def test_fused_moe_fp8_prefill_batch_sampled_rows():
     # 2048 tokens: the 8-wave 256x256 fp8 kernel with the tail's K splits
     T, H, I, E, k = 2048, 1024, 512, 8, 2
