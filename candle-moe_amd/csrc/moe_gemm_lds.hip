@@ -363,7 +363,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         scale_acc([&](int col) {
             const f32x4 up = *reinterpret_cast<const f32x4*>(s_unit + (j - 1) * BN + col);
             const f32x4 un = *reinterpret_cast<const f32x4*>(s_unit + j * BN + col);
-            return f32x4{up[0] / un[0], up[1] / un[1], up[2] / un[2], up[3] / un[3]};
+            // reciprocal to ~1 ulp: the units cancel to that accuracy in
+            // the end, far below the fp8 codes' own rounding
+            return f32x4{up[0] * __builtin_amdgcn_rcpf(un[0]), up[1] * __builtin_amdgcn_rcpf(un[1]),
+                         up[2] * __builtin_amdgcn_rcpf(un[2]), up[3] * __builtin_amdgcn_rcpf(un[3])};
         });
     };
     auto to_absolute = [&](int j) {
@@ -458,8 +461,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                                                      lh * 8);
         }
     };
-    auto compute_w8i = [&](int stage) {
-        if (!rows_live) return;
+    auto compute_w8i = [&](int stage, int ds, int dk) {
+        if (!rows_live) {
+#pragma unroll
+            for (int st = 0; st < KSTEPS; ++st) dma_slice(ds, dk, st);
+            return;
+        }
         const char* sA = smem + stage * STAGE;
         const char* sB = sA + A_BYTES;
         u32x4 af0[MB], af1[MB], bfr[NB];
@@ -475,19 +482,23 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         mfma_step(af0, bfr);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, 0);
         load_w8(sA, sB, 2, af0, br0);
         cvt(br1);
         mfma_step(af1, bfr);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, 1);
         load_w8(sA, sB, 3, af1, br1);
         cvt(br0);
         mfma_step(af0, bfr);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, 2);
         cvt(br1);
         mfma_step(af1, bfr);
         __builtin_amdgcn_sched_barrier(0);
+        dma_slice(ds, dk, KSTEPS - 1);
     };
     auto compute = [&](int stage, int ds, int dk) {
         if (!rows_live) {
@@ -640,6 +651,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
+    // fp8 expert sets: segment of the split's first K tile, and the K tile
+    // at which the next one starts (segments are seg_kt whole K tiles)
+    const int seg_kt = W8SET ? a.seg_len / BK : 1;
+    int seg_cur = W8SET ? kt0 / seg_kt : 0;
+    int seg_next = W8SET ? (seg_cur + 1) * seg_kt : 0;
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
         if (s < nk) issue(s, (kt0 + s) * BK);
@@ -649,19 +665,23 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         wait_lgkm0();
         block_barrier();
         const int ahead = kt + NST - 1;
-        // row group 1 issues after its first k16 step (not with fp8 weights,
-        // whose compute_w8 has no DMA slot)
-        const bool late = NW == 8 && !W8 && wm == 1;
+        // row group 1 issues after its first k16 step (the decode kernels'
+        // compute_w8 has no DMA slot)
+        const bool late = NW == 8 && (!W8 || KSTEPS == 4) && wm == 1;
         if (ahead < nk && !late) issue(ahead % NST, (kt0 + ahead) * BK);
         if constexpr (W8SET) {
             // fp8 expert sets: the accumulators hold the current segment's
             // column units; entering segment j they are rescaled by
             // u_{j-1} / u_j (the K tiles of a segment never straddle one:
             // seg_len is a multiple of BK)
-            const int kg = (kt0 + kt) * BK;
-            if (kt > 0 && rows_live && kg % a.seg_len == 0) rescale_units(kg / a.seg_len);
+            if (kt0 + kt == seg_next) {
+                if (kt > 0 && rows_live) rescale_units(seg_cur + 1);
+                ++seg_cur;
+                seg_next += seg_kt;
+            }
         }
-        if constexpr (W8 && NW == 8 && KSTEPS == 4) compute_w8i(kt % NST);
+        if constexpr (W8 && NW == 8 && KSTEPS == 4)
+            compute_w8i(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
         else if constexpr (W8) compute_w8(kt % NST);
         else compute(kt % NST, (late && ahead < nk) ? ahead % NST : -1, (kt0 + ahead) * BK);
     }
