@@ -49,8 +49,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + ["router", "fp8"],
-                    help="MoE layer (qwen3 headline, nomic, q30b), router alone, or fp8: the decode GEMMs with "
-                         "bf16 against fp8 expert weights only")
+                    help="MoE layer (qwen3 headline, nomic, q30b), router alone, or fp8: bf16 against fp8 "
+                         "expert weights only (the decode GEMMs, and whole prefill calls with their GEMMs)")
     ap.add_argument("--tokens", type=int, default=0, help="override T")
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
@@ -107,10 +107,12 @@ def main():
         return bench_router_only(args, torch, cm, dev)
     if args.workload == "fp8":
         res = bench_fp8_decode(torch, cm, dev, args)
+        pre = bench_fp8_prefill(torch, cm, dev, args)
         gu = [v["bf16"]["gemm_gate_up"] / v["fp8"]["gemm_gate_up"] for v in res.values()]
         print(json.dumps({"metric": "decode GEMM time, bf16 over fp8 e4m3 expert weights", "value": round(min(gu), 3),
                           "unit": "x (gate/up GEMM, worst shape)", "n_gpus": 1, "higher_is_better": True,
-                          "data": "synthetic", "config": {"workload": "fp8 decode GEMMs"}, "fp8_decode": res}))
+                          "data": "synthetic", "config": {"workload": "fp8 decode GEMMs"}, "fp8_decode": res,
+                          "fp8_prefill": pre}))
         return None
 
     wl = dict(WORKLOADS[args.workload])
@@ -488,6 +490,79 @@ def bench_fp8_decode(torch, cm, dev, args):
         entry["gemm_speedup"] = round((b["gemm_gate_up"] + b["gemm_down"]) / (f["gemm_gate_up"] + f["gemm_down"]), 3)
         res[f"{wname}_T{T}"] = entry
         del bf, f8
+    return res
+
+
+def bench_fp8_prefill(torch, cm, dev, args):
+    """Prefill with bf16 against fp8 e4m3 expert weights (Qwen3 T=4096 and
+    T=32768, Nomic T=32768): µs per call over 10 calls between two events —
+    bf16 the host FusedMoE::forward (router outputs given), fp8 the zeroing of
+    the output plus candle_moe_fused_moe_fp8 adding into it (its drop-in
+    form) — and each GEMM's µs per launch from a separate pass with HIP events
+    around every launch; rel_rms = RMS(fp8 output - bf16 output) / RMS(bf16
+    output), the weight quantization's effect on the layer."""
+    L = cm.lib()
+    nslots = L.candle_moe_profile_begin()
+    cm.check(L.candle_moe_profile_end(None, None, 0))
+    names = [L.candle_moe_profile_slot_name(s).decode() for s in range(nslots)]
+    res = {}
+    for wname, T in (("qwen3", 4096), ("qwen3", 32768), ("nomic", 32768)):
+        wl = WORKLOADS[wname]
+        H, I, E, k = wl["H"], wl["I"], wl["E"], wl["k"]
+        qwen3 = wl["moe_type"] == 0
+        act = {"silu": cm.Activation.Silu, "gelu": cm.Activation.Gelu, "relu": cm.Activation.Relu}[wl["act"]]
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + T)
+        x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+        gate = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        up = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        down = (torch.randn((E, I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16) if qwen3 else None
+        logits = torch.randn((T, E), generator=g, device=dev)
+        tw = torch.empty((T, k), device=dev)
+        ti = torch.empty((T, k), dtype=torch.int32, device=dev)
+        tei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        cm.apply_topk_softmax_inplace(logits, tw, ti, tei)
+        gq, gs = cm.quantize_fp8(gate, input_kn=True)
+        uq, us_ = cm.quantize_fp8(up, input_kn=qwen3)  # Nomic fc2 [E, H, I] is already [N, K]
+        dq, ds = cm.quantize_fp8(down, input_kn=True) if qwen3 else (None, None)
+        moe = cm.FusedMoE.new(E, k, act)
+        out8 = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+        def run_bf16():
+            return moe.forward(x, gate, up, down, tw, ti, wl["moe_type"])
+
+        def run_fp8():
+            out8.zero_()
+            cm.fused_moe_fp8(x, gq, uq, dq, gs, us_, ds, tw, ti, out8, E, k, int(act), wl["moe_type"])
+            return out8
+
+        entry = {"tokens": T}
+        outs = {}
+        for label, fn in (("bf16", run_bf16), ("fp8", run_fp8)):
+            for _ in range(3):
+                outs[label] = fn()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                fn()
+            e1.record()
+            e1.synchronize()
+            call_us = e0.elapsed_time(e1) / 10 * 1e3
+            L.candle_moe_profile_begin()
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            ms = (ctypes.c_double * nslots)()
+            cnt = (ctypes.c_int * nslots)()
+            cm.check(L.candle_moe_profile_end(ms, cnt, nslots))
+            us = {names[s]: round(1000.0 * ms[s] / cnt[s], 1) for s in range(nslots) if cnt[s] and "gemm" in names[s]}
+            entry[label] = {"call_us": round(call_us, 1), **us}
+        ref = outs["bf16"].float()
+        entry["rel_rms"] = round(float((outs["fp8"].float() - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()), 4)
+        res[f"{wname}_T{T}"] = entry
+        del x, gate, up, down, gq, uq, dq, out8, outs, ref
     return res
 
 
