@@ -182,6 +182,15 @@ constexpr double kSetMinRowBytes = 256.0 * 1024 * 1024;
 // (k*H*2 bytes per token against H*4), which bounds the workspace of shapes
 // whose expert sets are too many for the expert-set path (large k and E).
 constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
+// fp8 weights: most pairs for the register-operand decode kernel (kW8Gemv;
+// its workgroups re-stream an expert's weights per 32-row tile like the
+// 32-row kernel's, without that kernel's LDS stages and split-K fixup).
+// Measured against the 32-row kernel (fp8 GEMM µs, gate/up + down):
+// Qwen3-30B-A3B T=1 (8 pairs) 29.1 -> 21.4, Qwen3 T=16 (32 pairs) 51.2
+// against 50.5, Qwen3 T=64 65.2 against 51.3, Qwen3-30B-A3B T=16 (128 pairs
+// over ~30 experts) 51.6 against 40.2. (The host cannot tell how many
+// experts a batch touches, so the bound is on the pairs.)
+constexpr long long kW8GemvPairs = 16;
 static int g_combine_policy = 0;
 // 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
@@ -292,13 +301,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // least, the rows over the tile height at least.
     const long long touched = P < E ? P : E;
     auto est_tiles = [&](int bm) { return std::max<long long>((P + bm - 1) / bm, touched); };
-    p.cfg = !p.mfma ? kTileSimt : (g_tile_policy ? g_tile_policy : kLds256w8);
+    // (policy kW8Gemv concerns fp8 weights only: automatic here)
+    const int policy = g_tile_policy == kW8Gemv ? 0 : g_tile_policy;
+    p.cfg = !p.mfma ? kTileSimt : (policy ? policy : kLds256w8);
     // f32: the tiled vector-FMA kernel (32-row tile with K splits for decode,
     // 128-row tile otherwise) wherever 16-byte loads are possible
     const bool f32_tiled = p.dtype == kF32 && H % 4 == 0 && I % 4 == 0 && aligned16;
     if (f32_tiled) {
         p.cfg = (P <= 32 * touched) ? kF32Rows32 : kF32Tile128;
-        if (g_tile_policy == kF32Rows32 || g_tile_policy == kF32Tile128) p.cfg = g_tile_policy;
+        if (policy == kF32Rows32 || policy == kF32Tile128) p.cfg = policy;
     } else if (!p.mfma || is_f32_cfg(p.cfg)) {
         p.cfg = kTileSimt;
     }
@@ -307,10 +318,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             return set_error(CANDLE_MOE_ERR_UNSUPPORTED,
                              "fused_moe_fp8: needs f16 or bf16 activations, hidden_dim and intermediate_dim multiples "
                              "of 16 and 16-byte aligned tensors (got dtype %u, %d, %d)", dtype, H, I);
-        // the 32-row kernel streams each touched expert's weights once per
-        // row tile: decode batches; beyond, the 8-wave 256x256 kernel
-        p.cfg = (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
-    } else if (p.mfma && !g_tile_policy) {
+        // decode batches stream each touched expert's weights once per row
+        // tile: up to kW8GemvPairs pairs the register-operand kernel (no LDS
+        // staging, no K splits across workgroups), up to 32 rows per touched
+        // expert the 32-row tile kernel; beyond, the 8-wave 256x256 kernel.
+        // Tile policies 17, 12 and 7 force one of them.
+        p.cfg = (P <= kW8GemvPairs) ? kW8Gemv : (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
+        if (g_tile_policy == kW8Gemv || g_tile_policy == kLdsRows32 || g_tile_policy == kLds256w8)
+            p.cfg = g_tile_policy;
+    } else if (p.mfma && !policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
@@ -381,7 +397,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // Qwen3-30B-A3B shapes). Deterministic for every k. Not for the 32-row
     // decode kernels, whose few atomics cost less than the k-row pass
     // (Qwen3-30B-A3B T=16: 90 against 94 us).
-    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 &&
+    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 && p.cfg != kW8Gemv &&
                   (double)P * H * 2.0 <= kRowsMaxBytes;
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     // Decode fc1 (Nomic) likewise on 128-column tiles where the 256-column
@@ -405,6 +421,12 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
                               : gemm_tile_cols(kDown, p.cfg);
     p.narrow2 = down_cols == 128 && gemm_tile_cols(kDown, p.cfg) != 128;
     p.n_tiles2 = cdiv(H, down_cols);
+    if (p.cfg == kW8Gemv) {
+        // the grid of the split with the most workgroups (the kernel picks
+        // the split from the live row tiles)
+        p.n_tiles1 = cdiv(I, gv_wg_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, 4));
+        p.n_tiles2 = cdiv(H, gv_wg_cols(kDown, 4));
+    }
     p.split1 = p.split2 = 1;
     // tail balance for the 8-wave 256x256 kernel (its K splits meet in the
     // split-K fixup): the tiles of each XCD's last, partly filled round are
@@ -1037,7 +1059,7 @@ int candle_moe_set_grouping_mode(int mode) {
 int candle_moe_set_tile_policy(int policy) {
     if (policy < 0 || policy >= cm::kNumTileCfgs || !cm::is_shipped_cfg(policy))
         return cm::set_error(CANDLE_MOE_ERR_INVALID,
-                             "tile policy must be one of 0 (auto), 1, 5, 7, 12, 14, 15, 16 (got %d)", policy);
+                             "tile policy must be one of 0 (auto), 1, 5, 7, 12, 14, 15, 16, 17 (got %d)", policy);
     cm::g_tile_policy = policy;
     return CANDLE_MOE_OK;
 }

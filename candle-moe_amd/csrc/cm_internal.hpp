@@ -141,32 +141,53 @@ constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter s
 //   kLdsRows32: 32x256, 4 waves side by side along N, BK 64, 4 stages: few
 //     rows per expert (decode), bound by streaming the weights;
 //   kLds128x256o2: 128x256, 4 waves, BK 32, 3 stages, two workgroups per CU.
+// kW8Gemv (fp8 weights only, moe_gemv_w8.hip): the 32-row tile table, 16
+//   output columns (gate/up) or 32 per workgroup over the whole of K, split
+//   over its 4 waves; operands loaded straight into registers (decode).
 // f32 vector-FMA kernels (moe_gemm_f32.hip): kF32Rows32 (32x128 block tile),
 //   kF32Tile128 (128x128).
 // The grouping's tile table must be built with the kernel's row tile,
 // tile_rows().
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kLds128 = 5, kLds256w8 = 7, kLdsRows32 = 12, kLds128x256o2 = 14,
-    kF32Rows32 = 15, kF32Tile128 = 16
+    kF32Rows32 = 15, kF32Tile128 = 16, kW8Gemv = 17
 };
-constexpr int kNumTileCfgs = 17;  // codes are < kNumTileCfgs
+constexpr int kNumTileCfgs = 18;  // codes are < kNumTileCfgs
 inline bool is_shipped_cfg(int cfg) {
     return cfg == kTileSimt || cfg == kTile128 || cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 ||
-           cfg == kLds128x256o2 || cfg == kF32Rows32 || cfg == kF32Tile128;
+           cfg == kLds128x256o2 || cfg == kF32Rows32 || cfg == kF32Tile128 || cfg == kW8Gemv;
 }
 inline bool is_f32_cfg(int cfg) { return cfg == kF32Rows32 || cfg == kF32Tile128; }
 inline int tile_rows(int cfg) {
-    if (cfg == kLdsRows32 || cfg == kF32Rows32) return 32;
+    if (cfg == kLdsRows32 || cfg == kF32Rows32 || cfg == kW8Gemv) return 32;
     if (cfg == kTileSimt) return 64;
     if (cfg == kLds256w8) return 256;
     return 128;  // kTile128, kLds128, kLds128x256o2, kF32Tile128
 }
+// kW8Gemv: 16-column blocks per wave; output columns of a workgroup whose 4
+// waves split K in kw parts; kw for a GEMM of K, N over `tiles` row tiles:
+// the fewest K parts (1, 2, 4) that still give 512 workgroups (two per CU),
+// else 4.
+constexpr int kGvCB = 2;
+__host__ __device__ inline int gv_wg_cols(int mode, int kw) {
+    return (mode == kGateUp ? 8 * kGvCB : 16 * kGvCB) * (4 / kw);
+}
+__host__ __device__ inline int gv_pick_kw(int mode, int N, long long tiles) {
+    for (int kw = 1; kw < 4; kw *= 2)
+        if (tiles * ((N + gv_wg_cols(mode, kw) - 1) / gv_wg_cols(mode, kw)) >= 512) return kw;
+    return 4;
+}
 inline int tile_cols(int cfg) {
     if (cfg == kTileSimt) return 64;
+    if (cfg == kW8Gemv) return 16 * kGvCB;
     if (cfg == kLds256w8 || cfg == kLdsRows32 || cfg == kLds128x256o2) return 256;
     return 128;  // kTile128, kLds128, f32 kernels
 }
-inline bool is_lds_cfg(int cfg) { return cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 || cfg == kLds128x256o2; }
+// (kW8Gemv shares the LDS-DMA kernels' 32-bit buffer offsets and fused
+// accumulator clear)
+inline bool is_lds_cfg(int cfg) {
+    return cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 || cfg == kLds128x256o2 || cfg == kW8Gemv;
+}
 // Workgroups of a launch over at most `tiles` output tiles: with adaptive K
 // splits live tiles * splits stays within split_target when it splits.
 inline long long split_grid(long long tiles, const GemmArgs& a) {
@@ -189,8 +210,11 @@ hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, 
 // = K, strideB = N*K) with per-output-column scales (scale0 / scale1), on the
 // 32-row kernel (tile_rows(kLdsRows32)); 16-bit activations; modes kGateUp,
 // kFc1, kDown, kFc2.
-// cfg: kLdsRows32 (decode) or kLds256w8
+// cfg: kW8Gemv or kLdsRows32 (decode), or kLds256w8
 hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream);
+// kW8Gemv (moe_gemv_w8.hip): modes kGateUp, kFc1, kDown, kFc2 (pair path,
+// f32 atomics for kDown / kFc2)
+hipError_t launch_w8_gemv(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
 

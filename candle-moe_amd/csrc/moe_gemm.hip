@@ -631,7 +631,7 @@ bool mfma_supported(int dtype, int K, int N) {
 
 int gemm_tile_cols(int mode, int cfg) {
     const int bn = tile_cols(cfg);
-    if (is_f32_cfg(cfg)) return mode == kGateUp ? bn / 2 : bn;
+    if (is_f32_cfg(cfg) || cfg == kW8Gemv) return mode == kGateUp ? bn / 2 : bn;
     return (mode == kGateUp && cfg != kTileSimt) ? bn / 2 : bn;
 }
 

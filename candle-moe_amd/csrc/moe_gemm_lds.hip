@@ -829,6 +829,7 @@ static hipError_t launch_w8_dt(int mode, int cfg, const GemmArgs& a, hipStream_t
     }
 }
 hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
+    if (cfg == kW8Gemv) return launch_w8_gemv(mode, dtype, a, stream);
     if (dtype == kBF16) return launch_w8_dt<kBF16>(mode, cfg, a, stream);
     if (dtype == kF16) return launch_w8_dt<kF16>(mode, cfg, a, stream);
     return hipErrorInvalidValue;

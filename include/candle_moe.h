@@ -171,6 +171,11 @@ int candle_moe_set_combine_policy(int policy);
  * when the tiles are few; by default 15 for <= 32 rows per expert, else 16
  * (the scalar 64x64 kernel 0 when hidden_dim or intermediate_dim is not a
  * multiple of 4 or an operand is not 16-byte aligned).
+ * 17 concerns fp8 weights only (candle_moe_fused_moe_fp8; fused_moe
+ * treats it as 0): the register-operand decode kernel, taken by default for
+ * at most 16 pairs (num_tokens x num_selected_experts); for fp8 weights 12
+ * and 7 force the 32-row and the 256x256 kernel, other codes leave the fp8
+ * choice automatic.
  * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
 int candle_moe_set_tile_policy(int policy);
 

@@ -217,14 +217,25 @@ def test_default_path_and_kernel(T, H, I, E, k, mt, path, kernel, rows):
 
 
 def test_tile_policy_accepts_only_shipped_kernels():
-    for code in cm.TILE_CODES:
+    for code in cm.TILE_CODES + (cm.TILE_W8_GEMV,):
         cm.set_tile_policy(code)
     cm.set_tile_policy(0)
-    for code in (2, 3, 4, 6, 8, 9, 10, 11, 13, 17, -1):
+    for code in (2, 3, 4, 6, 8, 9, 10, 11, 13, 18, -1):
         with pytest.raises(cm.CandleMoeError) as e:
             cm.set_tile_policy(code)
         assert e.value.code == cm.CANDLE_MOE_ERR_INVALID
     cm.set_tile_policy(0)
+
+
+def test_fp8_kernel_policy_leaves_fused_moe_automatic():
+    # policy 17 (fp8 register-operand decode kernel) does not change fused_moe's choice
+    shapes = [(16, 4096, 1536, 8, 2), (32768, 4096, 1536, 8, 2), (512, 768, 3072, 8, 2)]
+    auto = [cm.fused_moe_kernel(*s, 1, 0) for s in shapes]
+    cm.set_tile_policy(cm.TILE_W8_GEMV)
+    try:
+        assert [cm.fused_moe_kernel(*s, 1, 0) for s in shapes] == auto
+    finally:
+        cm.set_tile_policy(0)
 
 
 def test_grouping_mode_setter():

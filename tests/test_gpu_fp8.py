@@ -138,6 +138,43 @@ def test_fused_moe_fp8_matches_oracle(name, T, H, I, E, k, act, mt, dt, zipf):
     assert_close(got, want, RTOL[dt], f"{name} fp8 vs f64 oracle on the dequantized weights")
 
 
+# The register-operand decode kernel (tile policy 17; by default only up to
+# 16 pairs) forced on every decode case: K and N tails, tiles
+# of more than 16 rows (two row blocks) and more than 32 (several tiles per
+# expert), f16, Nomic's fc1 / fc2, and accumulate mode with dropped pairs.
+GEMV_CASES = CASES + [
+    ("qwen3_rows24_T48", 48, 1024, 512, 4, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("qwen3_skew_T96", 96, 512, 256, 8, 2, O.SILU, O.QWEN3, O.BF16, 2.0),
+]
+
+
+@pytest.mark.parametrize("name,T,H,I,E,k,act,mt,dt,zipf", GEMV_CASES, ids=[c[0] for c in GEMV_CASES])
+def test_fused_moe_fp8_register_operand_kernel(name, T, H, I, E, k, act, mt, dt, zipf):
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, zipf, seed=150 + T)
+    candle_moe.set_tile_policy(candle_moe.TILE_W8_GEMV)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
+    assert_close(got, want, RTOL[dt], f"{name} register-operand fp8 kernel vs f64 oracle")
+
+
+def test_fused_moe_fp8_register_operand_kernel_accumulates_and_drops():
+    T, H, I, E, k = 24, 512, 256, 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=93)
+    ri = ri.copy()
+    ri[::3, 1] = E + 5
+    init = O.to_dtype(O.randn((T, H), seed=94, std=0.5), O.BF16)
+    candle_moe.set_tile_policy(candle_moe.TILE_W8_GEMV)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init)
+    assert_close(got, want, RTOL[O.BF16], "register-operand fp8 kernel, accumulate mode with dropped pairs")
+
+
 @pytest.mark.parametrize("mt", [O.QWEN3, O.NOMIC])
 def test_fused_moe_fp8_accumulates(mt):
     T, H, I, E, k = (16, 4096, 1536, 8, 2) if mt == O.QWEN3 else (16, 768, 3072, 8, 2)
