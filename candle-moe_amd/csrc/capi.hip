@@ -415,8 +415,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // 16 / 64 18.5 -> 16.8, 24.0 -> 21.9, 25.0 -> 23.1 us, Nomic T=16 / 64
     // 16.0 -> 13.6, 16.5 -> 14.2 us. With I = 768 (Qwen3-30B-A3B) or live
     // tiles enough for every CU the wide tiles stay ahead (T=1: 13.1 against
-    // 13.6 us, T=16: 50.6 against 56.1 us).
-    const int down_cols = (p.cfg == kLdsRows32 && !fp8 && I >= 1536 && touched * cdiv(H, 256) < dev_wgs)
+    // 13.6 us, T=16: 50.6 against 56.1 us). fp8 weights the same: Qwen3 T=16
+    // / 64 20.4 -> 16.2, 20.5 -> 16.6 us.
+    const int down_cols = (p.cfg == kLdsRows32 && I >= 1536 && touched * cdiv(H, 256) < dev_wgs)
                               ? 128
                               : gemm_tile_cols(kDown, p.cfg);
     p.narrow2 = down_cols == 128 && gemm_tile_cols(kDown, p.cfg) != 128;

@@ -782,7 +782,8 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// fp8-weight GEMMs, pair-path modes only: the 32-row kernel (decode) or the
+// fp8-weight GEMMs, pair-path modes only: the 32-row kernel (decode; down /
+// fc2 also on 128-column tiles, a.narrow) or the
 // 8-wave 256x256 kernel with 3 LDS stages (48 KB each: the fp8 B tile is half
 // the 16-bit one) for larger batches
 template <int DT, int MODE>
@@ -809,6 +810,13 @@ static hipError_t launch_w8_mode(int cfg, const GemmArgs& a, hipStream_t stream)
 #ifndef CM_W8_OCC
 #define CM_W8_OCC 1
 #endif
+    if constexpr (MODE == kDown || MODE == kFc1) {
+        if (a.narrow) {  // 128-column tiles (n_tiles counts those)
+            hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, CM_W8_NST, 4, MODE, 1, CM_W8_OCC, true>),
+                               dim3((int)nwg_l), dim3(256), 0, stream, a);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, CM_W8_NST, 4, MODE, 1, CM_W8_OCC, true>), dim3((int)nwg_l),
                        dim3(256), 0, stream, a);
     return hipGetLastError();
