@@ -52,6 +52,8 @@ def parse():
                     help="MoE layer (qwen3 headline, nomic, q30b), router alone, or fp8: bf16 against fp8 "
                          "expert weights only (the decode GEMMs, and whole prefill calls with their GEMMs)")
     ap.add_argument("--tokens", type=int, default=0, help="override T")
+    ap.add_argument("--fp8-shape", default="", choices=["", "qwen3_T16", "qwen3_T64", "q30b_T1", "q30b_T16"],
+                    help="fp8 workload: this decode shape only (no prefill calls), e.g. for a per-shape kernel trace")
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-sample", type=int, default=32768,
@@ -107,7 +109,7 @@ def main():
         return bench_router_only(args, torch, cm, dev)
     if args.workload == "fp8":
         res = bench_fp8_decode(torch, cm, dev, args)
-        pre = bench_fp8_prefill(torch, cm, dev, args)
+        pre = None if args.fp8_shape else bench_fp8_prefill(torch, cm, dev, args)
         gu = [v["bf16"]["gemm_gate_up"] / v["fp8"]["gemm_gate_up"] for v in res.values()]
         print(json.dumps({"metric": "decode GEMM time, bf16 over fp8 e4m3 expert weights", "value": round(min(gu), 3),
                           "unit": "x (gate/up GEMM, worst shape)", "n_gpus": 1, "higher_is_better": True,
@@ -435,6 +437,8 @@ def bench_fp8_decode(torch, cm, dev, args):
     names = [L.candle_moe_profile_slot_name(s).decode() for s in range(nslots)]
     res = {}
     for wname, T in [("qwen3", 16), ("qwen3", 64), ("q30b", 1), ("q30b", 16)]:
+        if getattr(args, "fp8_shape", "") and args.fp8_shape != f"{wname}_T{T}":
+            continue
         wl = WORKLOADS[wname]
         H, I, E, k = wl["H"], wl["I"], wl["E"], wl["k"]
         g = torch.Generator(device=dev)
