@@ -52,7 +52,7 @@ def parse():
                     help="MoE layer (qwen3 headline, nomic, q30b), router alone, or fp8: bf16 against fp8 "
                          "expert weights only (the decode GEMMs, and whole prefill calls with their GEMMs)")
     ap.add_argument("--tokens", type=int, default=0, help="override T")
-    ap.add_argument("--fp8-shape", default="", choices=["", "qwen3_T16", "qwen3_T64", "q30b_T1", "q30b_T16"],
+    ap.add_argument("--fp8-shape", default="", choices=["", "qwen3_T16", "qwen3_T64", "q30b_T1", "q30b_T16", "nomic_T16"],
                     help="fp8 workload: this decode shape only (no prefill calls), e.g. for a per-shape kernel trace")
     ap.add_argument("--dtype", default="", choices=["", "bf16", "f16", "f32"])
     ap.add_argument("--seed", type=int, default=1234)
@@ -436,11 +436,13 @@ def bench_fp8_decode(torch, cm, dev, args):
     cm.check(L.candle_moe_profile_end(None, None, 0))
     names = [L.candle_moe_profile_slot_name(s).decode() for s in range(nslots)]
     res = {}
-    for wname, T in [("qwen3", 16), ("qwen3", 64), ("q30b", 1), ("q30b", 16)]:
+    for wname, T in [("qwen3", 16), ("qwen3", 64), ("q30b", 1), ("q30b", 16), ("nomic", 16)]:
         if getattr(args, "fp8_shape", "") and args.fp8_shape != f"{wname}_T{T}":
             continue
         wl = WORKLOADS[wname]
         H, I, E, k = wl["H"], wl["I"], wl["E"], wl["k"]
+        qwen3 = wl["moe_type"] == 0
+        act = {"silu": 0, "gelu": 1, "relu": 2}[wl["act"]]
         g = torch.Generator(device=dev)
         g.manual_seed(args.seed + T)
         ncopy = max(2, -(-(1024 << 20) // (3 * E * H * I)))  # fp8 bytes of all copies >= 1 GiB
@@ -457,20 +459,24 @@ def bench_fp8_decode(torch, cm, dev, args):
         touched = int(torch.unique(ti).numel())
         bf, f8 = [], []
         for _ in range(ncopy):
-            w3 = [(torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-                  for shape in ((E, H, I), (E, H, I), (E, I, H))]
+            # Qwen3: gate/up [E,H,I], down [E,I,H]; Nomic: fc1 [E,H,I], fc2 [E,H,I] (already [N,K])
+            shapes = ((E, H, I), (E, H, I), (E, I, H)) if qwen3 else ((E, H, I), (E, H, I))
+            w3 = [(torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16) for shape in shapes]
+            if not qwen3:
+                w3.append(None)
             bf.append(w3)
-            f8.append([cm.quantize_fp8(w, input_kn=True) for w in w3])
+            f8.append([cm.quantize_fp8(w, input_kn=(qwen3 or j == 0)) if w is not None else (None, None)
+                       for j, w in enumerate(w3)])
         out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
 
         def run(fp8, c):
             if fp8:
                 (gq, gs), (uq, us_), (dq, ds) = f8[c]
                 return L.candle_moe_fused_moe_fp8(p(x), p(gq), p(uq), p(dq), p(gs), p(us_), p(ds), p(tw), p(ti),
-                                                  p(out), T, H, I, E, k, 0, 0, 1, stream)
+                                                  p(out), T, H, I, E, k, act, wl["moe_type"], 1, stream)
             gw, uw, dw = bf[c]
-            return L.candle_moe_fused_moe_status(p(x), p(gw), p(uw), p(dw), p(tw), p(ti), p(out), T, H, I, E, k, 0,
-                                                 0, 1, stream)
+            return L.candle_moe_fused_moe_status(p(x), p(gw), p(uw), p(dw), p(tw), p(ti), p(out), T, H, I, E, k, act,
+                                                 wl["moe_type"], 1, stream)
 
         entry = {"tokens": T, "touched_experts": touched, "weight_copies": ncopy}
         for label, fp8 in (("bf16", False), ("fp8", True)):
@@ -486,7 +492,7 @@ def bench_fp8_decode(torch, cm, dev, args):
             cm.check(L.candle_moe_profile_end(ms, cnt, nslots))
             us = {names[s]: round(1000.0 * ms[s] / cnt[s], 2) for s in range(nslots) if cnt[s]}
             bpe = 1 if fp8 else 2
-            g1b, g2b = touched * 2 * H * I * bpe, touched * H * I * bpe
+            g1b, g2b = touched * (2 if qwen3 else 1) * H * I * bpe, touched * H * I * bpe
             us["gate_up_gbs"] = round(g1b / (us["gemm_gate_up"] * 1e-6) / 1e9, 1)
             us["down_gbs"] = round(g2b / (us["gemm_down"] * 1e-6) / 1e9, 1)
             entry[label] = us
