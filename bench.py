@@ -58,9 +58,10 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-sample", type=int, default=32768,
                     help="tokens in the CPU-baseline sample (0 = skip; default: the whole batch)")
-    ap.add_argument("--tile", type=int, default=0, choices=[0, 1, 5, 7, 12, 14, 15, 16],
+    ap.add_argument("--tile", type=int, default=0, choices=[0, 1, 5, 7, 12, 14, 15, 16, 17],
                     help="GEMM kernel: 0 auto, 1 register-staged 128x128, 5 LDS-DMA 128x128, 7 LDS-DMA 256x256 "
-                         "8 waves, 12 32-row (decode), 14 128x256 two workgroups per CU, 15/16 f32 32-row / 128-row")
+                         "8 waves, 12 32-row (decode), 14 128x256 two workgroups per CU, 15/16 f32 32-row / 128-row, "
+                         "17 fp8 register-operand decode kernel (--workload fp8)")
     ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
