@@ -106,6 +106,8 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_noalloc.restype = i32
         L.candle_moe_fused_moe_noalloc_scratch_bytes.argtypes = []
         L.candle_moe_fused_moe_noalloc_scratch_bytes.restype = sz
+        L.candle_moe_test_router_exp.argtypes = [u32, u32, vp, vp]
+        L.candle_moe_test_router_exp.restype = i32
         L.candle_moe_quantize_fp8.argtypes = [vp, u32, i32, i32, i32, i32, vp, vp, vp]
         L.candle_moe_quantize_fp8.restype = i32
         L.candle_moe_dequantize_fp8.argtypes = [vp, vp, i32, i32, i32, vp, u32, vp]
@@ -331,9 +333,46 @@ def fused_moe_fp8(input, gate_q, up_q, down_q, gate_scale, up_scale, down_scale,
     up as for fused_moe): gate_q = fc1 [E, I, H] with gate_scale [E, I], up_q =
     fc2 [E, H, I] with up_scale [E, H] (down_q and down_scale None).
     input/output [T, H] f16 or bf16; routing_weights
-    [T, k] f32; expert_indices [T, k] u32/i32."""
+    [T, k] f32; expert_indices [T, k] u32/i32. Every tensor must be
+    contiguous and on input's device; the codes are uint8 and the scales f32
+    of the shapes above (the C entry point takes raw pointers and cannot check
+    them), else CandleMoeError."""
+    import torch
+
+    def bad(msg):
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "fused_moe_fp8: " + msg)
+
+    if input.dim() != 2 or gate_q.dim() != 3:
+        bad("input must be [T, H] and gate_q [E, I, H]")
     T, H = input.shape
-    I = gate_q.shape[1]
+    E, I = num_experts, gate_q.shape[1]
+    qwen3 = moe_type == 0
+    codes = {"gate_q": (gate_q, (E, I, H)), "up_q": (up_q, (E, I, H) if qwen3 else (E, H, I))}
+    scales = {"gate_scale": (gate_scale, (E, I)), "up_scale": (up_scale, (E, I) if qwen3 else (E, H))}
+    if qwen3:
+        codes["down_q"] = (down_q, (E, H, I))
+        scales["down_scale"] = (down_scale, (E, H))
+    elif down_q is not None or down_scale is not None:
+        bad("Nomic (moe_type 1) takes no down_q / down_scale")
+    rest = {"routing_weights": (routing_weights, (T, top_k)), "expert_indices": (expert_indices, (T, top_k)),
+            "output": (output, (T, H))}
+    for group, dtypes in ((codes, (torch.uint8,)), (scales, (torch.float32,)),
+                          ({"routing_weights": rest["routing_weights"]}, (torch.float32,)),
+                          ({"expert_indices": rest["expert_indices"]}, (torch.int32, torch.uint32)),
+                          ({"output": rest["output"]}, (input.dtype,))):
+        for name, (t, shape) in group.items():
+            if t is None:
+                bad(f"{name} is missing")
+            if tuple(t.shape) != tuple(shape):
+                bad(f"{name} must be {list(shape)}, got {list(t.shape)}")
+            if t.dtype not in dtypes:
+                bad(f"{name} must be {' or '.join(str(d) for d in dtypes)}, got {t.dtype}")
+            if not t.is_contiguous():
+                bad(f"{name} must be contiguous")
+            if t.device != input.device:
+                bad(f"{name} must be on {input.device}, got {t.device}")
+    if not input.is_contiguous():
+        bad("input must be contiguous")
     p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
     check(lib().candle_moe_fused_moe_fp8(
         p(input), p(gate_q), p(up_q), p(down_q), p(gate_scale), p(up_scale), p(down_scale), p(routing_weights),

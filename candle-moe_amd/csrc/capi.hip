@@ -196,7 +196,7 @@ static int g_combine_policy = 0;
 static int g_tile_policy = 0;
 // Grouping launches above kGroupSmallMax items: 0 one launch where the
 // workspace's counters are known to start at zero (library-owned
-// workspaces, the no-allocation scratch) and the launch fits the device,
+// workspaces, each used by one stream) and the launch fits the device,
 // else two; 1 always two; 2 one launch whose workgroups all take the recount
 // fallback (tests).
 static int g_grouping_mode = 0;
@@ -441,10 +441,6 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         auto bound = [&](int K) { return std::max(1, std::min(8, cdiv(K, bk))); };
         if (!p.set_path) p.split2 = bound(I);
         p.split1 = bound(H);
-#ifndef CM_W8_SPLITX
-#define CM_W8_SPLITX 1
-#endif
-        if (fp8) p.split_target = (int)(p.split_target * (CM_W8_SPLITX));
     } else if (is_f32_cfg(p.cfg) && P > 0) {
         const long long mt = est_tiles(p.BM);
         const int bk = tile_bk(p.cfg);
@@ -827,9 +823,15 @@ int fused_moe_noalloc_impl(const void* x, const void* gate, const void* up, cons
     rc = scratch_of_current_device(&ws);
     if (rc) return rc;
     // every piece of the layout that must start at zero (split-K arrival
-    // counters, the f32 accumulator) is cleared by this call's own kernels
+    // counters, the f32 accumulator) is cleared by this call's own kernels.
+    // The grouping takes its two-launch form (sync_zero false): the one-launch
+    // form counts workgroups in and out on counters that the previous launch
+    // leaves at zero, and on this array shared by every call on the GPU an
+    // overlapping call could leave them nonzero for the calls after it.
+    // Batches of up to kGroupSmallMax pairs (decode) take the one-workgroup
+    // grouping either way.
     return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
-                   out, false, reinterpret_cast<char*>(ws), reinterpret_cast<hipStream_t>(stream), nullptr, true);
+                   out, false, reinterpret_cast<char*>(ws), reinterpret_cast<hipStream_t>(stream), nullptr, false);
 }
 
 size_t fused_moe_ws_size(int T, int H, int I, int E, int k, uint32_t dtype) {
@@ -1037,6 +1039,13 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
                                                 reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k,
                                                 reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "router_topk launch");
+}
+
+int candle_moe_test_router_exp(uint32_t first_bits, uint32_t count, uint32_t* stats, void* stream) {
+    cm::clear_error();
+    if (!stats) return cm::set_error(CANDLE_MOE_ERR_INVALID, "test_router_exp: null stats pointer");
+    const hipError_t e = cm::launch_router_exp_check(first_bits, count, stats, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "test_router_exp launch");
 }
 
 int candle_moe_trim_workspaces(void) {

@@ -12,6 +12,8 @@ hipError_t launch_router_topk(const void* x, const void* w, int dtype, float* wo
                               int H, int E, int k, hipStream_t stream);
 hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_dtype, uint32_t* idx,
                                uint32_t* ei, int T, int E, int k, hipStream_t stream);
+// test support: the router's f32 exponential against its f64 one
+hipError_t launch_router_exp_check(uint32_t first, uint32_t n, uint32_t* stats, hipStream_t stream);
 
 // -------------------------------------------------------------- grouping
 // Pairs p = t*k + j are grouped by expert idx[p] (stable: ascending p inside

@@ -153,13 +153,16 @@ __device__ __forceinline__ u32x4 fp8x8_to(const u32x2& v) {
 // that arrives last sums all partials in split order (so the result does not
 // depend on which split finished last), resets the counter and returns true
 // (it runs the epilogue, once per tile), the others return false. The splits
-// may run on different XCDs, whose L2s are not coherent with each other: the
-// partials are written and read with device-coherent buffer accesses (cache
-// policy sc1: written through to, and read from, the level shared by all
-// XCDs), each thread waits for its stores before the workgroup counts
-// itself, so no L2-wide write-back or invalidate is needed. The accesses are
-// compiler builtins, not inline asm: the stores read MFMA results, whose
-// read-after-write hazards only the compiler knows to pad.
+// may run on different XCDs, whose L2s are not coherent with each other. The
+// ordering is the memory model's: every thread's partial stores precede the
+// workgroup barrier, which precedes thread 0's acquire-release increment at
+// agent scope; the last split's increment reads every earlier one (one
+// release sequence), and its partial loads follow it after a second barrier.
+// The partials are also written and read with device-coherent buffer
+// accesses (cache policy sc1: written through to, and read from, the level
+// shared by all XCDs). The accesses are compiler builtins, not inline asm:
+// the stores read MFMA results, whose read-after-write hazards only the
+// compiler knows to pad.
 constexpr int kCachePolicyDevice = 16;  // CPol::SC1
 
 // PAIRED: the partials of two splits are loaded per round (the 32-row
@@ -183,10 +186,9 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB
                          __float_as_uint(r[i + 3])};
         __builtin_amdgcn_raw_buffer_store_b128(v, pr, mine + q * 1024, 0, kCachePolicyDevice);
     }
-    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(a.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+        s_last = __hip_atomic_fetch_add(a.counters + ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
     __syncthreads();
     if (!s_last) return false;
     // split 0 replaces the registers, the others add in split order

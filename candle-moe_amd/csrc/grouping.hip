@@ -502,14 +502,19 @@ template <bool TOK, int K>
 __device__ void one_launch_body(const GroupJob& j, int blk, int32_t* s_mem, int32_t* sync, int spin) {
     __shared__ int s_ok;
     hist_body<TOK, K, true>(j, blk, s_mem);
-    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this thread's count stores are done
+    // Publication: every thread's count stores precede the barrier, the
+    // barrier precedes thread 0's release increment (agent scope), and a
+    // workgroup whose acquire poll reads the job's total synchronises with
+    // every increment before it (the increments form one release sequence),
+    // so its reads of the count table after the next barrier see every
+    // block's counts.
     __syncthreads();
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         int ok = 0;
         if (spin >= 0) {
             for (int it = 0;; ++it) {
-                ok = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= j.nb;
+                ok = __hip_atomic_load(sync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= j.nb;
                 if (ok || it >= spin) break;
                 __builtin_amdgcn_s_sleep(2);
             }
@@ -519,7 +524,9 @@ __device__ void one_launch_body(const GroupJob& j, int blk, int32_t* s_mem, int3
     __syncthreads();
     scatter_body<TOK, K>(j, blk, s_mem, s_ok ? kCountsCoherent : kCountsRecount);
     if (threadIdx.x == 0) {
-        const int out = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // (acquire-release: the last one out resets the counters after every
+        // other workgroup's poll of sync[0])
+        const int out = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         if (out == j.nb - 1) {
             __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -174,10 +174,11 @@ __global__ __launch_bounds__(256, 2) void moe_f32_gemm(GemmArgs a) {
                              __float_as_uint(flat[4 * q + 2]), __float_as_uint(flat[4 * q + 3])};
             __builtin_amdgcn_raw_buffer_store_b128(v, pr, mine + q * 4096u, 0, kCachePolicyDevice);
         }
-        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        // stores -> barrier -> acquire-release increment at agent scope (as
+        // splitk_fixup): the last split's partial loads see every split's stores
         __syncthreads();
         if (tid == 0)
-            s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                      nsplit - 1;
         __syncthreads();
         if (!s_last) return;

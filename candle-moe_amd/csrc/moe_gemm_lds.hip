@@ -804,20 +804,17 @@ static hipError_t launch_w8_mode(int cfg, const GemmArgs& a, hipStream_t stream)
     const long long nwg_l = split_grid(tiles, a);
     if (nwg_l > 0x7fffffffLL) return hipErrorInvalidValue;
     if (nwg_l <= 0) return hipSuccess;
-#ifndef CM_W8_NST
-#define CM_W8_NST 4
-#endif
-#ifndef CM_W8_OCC
-#define CM_W8_OCC 1
-#endif
+    // 4 LDS stages of 20 KB, one workgroup per CU (6 or 7 stages, and two
+    // workgroups per CU, measured slower)
+    constexpr int kW8Nst = 4, kW8Occ = 1;
     if constexpr (MODE == kDown || MODE == kFc1) {
         if (a.narrow) {  // 128-column tiles (n_tiles counts those)
-            hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, CM_W8_NST, 4, MODE, 1, CM_W8_OCC, true>),
+            hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, kW8Nst, 4, MODE, 1, kW8Occ, true>),
                                dim3((int)nwg_l), dim3(256), 0, stream, a);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, CM_W8_NST, 4, MODE, 1, CM_W8_OCC, true>), dim3((int)nwg_l),
+    hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, kW8Nst, 4, MODE, 1, kW8Occ, true>), dim3((int)nwg_l),
                        dim3(256), 0, stream, a);
     return hipGetLastError();
 }

@@ -64,7 +64,6 @@ __device__ __forceinline__ void gemv_rows(const GemmArgs& a, int r0, int e, int 
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
     constexpr bool ATOMIC = (MODE == kDown);
-    constexpr int CW = kGvWaves / KW;
     const int lane = (int)(threadIdx.x & 63u);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int kq = wave % KW, cw = wave / KW;

@@ -1094,3 +1094,43 @@ hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_
 }
 
 }  // namespace cm
+
+namespace cm {
+
+// Test support (candle_moe_test_router_exp): the f32 exponential of the
+// router's f32 softmax against the f64 one, for the n f32 values whose bit
+// patterns are first, first + 1, ... (any sign and exponent): stats[0] =
+// the largest distance in units in the last place (bit patterns of the two
+// results as integers), stats[1] = how many inputs differ at all. Grid-stride
+// loop; every lane evaluates both functions and the wave folds its results
+// before one lane updates stats with vector atomics.
+__global__ __launch_bounds__(256) void router_exp_check_k(uint32_t first, uint32_t n, uint32_t* stats) {
+    uint32_t worst = 0, differ = 0;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float d = __uint_as_float(first + i);
+        const uint32_t a = __float_as_uint(exp_f32_fast(d));
+        const uint32_t b = __float_as_uint(exp_f32_f64(d));
+        const uint32_t dist = a > b ? a - b : b - a;
+        worst = dist > worst ? dist : worst;
+        differ += dist != 0;
+        if (i > 0xffffffffu - stride) break;  // (i + stride would wrap)
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t w2 = __shfl_xor(worst, off);
+        worst = w2 > worst ? w2 : worst;
+        differ += __shfl_xor(differ, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicMax(stats, worst);
+        atomicAdd(stats + 1, differ);
+    }
+}
+
+hipError_t launch_router_exp_check(uint32_t first, uint32_t n, uint32_t* stats, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(router_exp_check_k, dim3(2048), dim3(256), 0, stream, first, n, stats);
+    return hipGetLastError();
+}
+
+}  // namespace cm

@@ -121,8 +121,7 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
 
 /* fused_moe that allocates nothing, for callers that cannot allocate (code
  * under HIP graph capture, serving loops that must not call hipMalloc,
- * harnesses that forbid it). No counterpart in the reference, whose fused_moe
- * allocates its workspace per call (/root/reference/kernels/moe.cu:570,770).
+ * harnesses that forbid it). It has no counterpart in the reference.
  * Same arguments and result as candle_moe_fused_moe_status (output is added
  * into); the workspace is a fixed device array inside the library, one per
  * GPU, of candle_moe_fused_moe_noalloc_scratch_bytes() bytes (32 MiB: decode
@@ -131,7 +130,10 @@ int candle_moe_fused_moe_ws(const void* input, const void* gate_weights, const v
  * CANDLE_MOE_ERR_WORKSPACE before anything is launched. All calls on one GPU
  * share that array: calls that may overlap on one GPU (other streams, other
  * host threads without ordering) race and must be serialised by the caller.
- * Each call clears what must start at zero; nothing else carries over. */
+ * Each call clears, with its own kernels, every piece of the array that must
+ * start at zero (split-K arrival counters, accumulators); no call depends on
+ * what an earlier call left in the array, so a race between overlapping calls
+ * corrupts only their own outputs. */
 int candle_moe_fused_moe_noalloc(const void* input, const void* gate_weights, const void* up_weights,
                                  const void* down_weights, const void* routing_weights,
                                  const void* expert_indices, void* output, int num_tokens,
@@ -214,6 +216,14 @@ int candle_moe_fused_moe_path_ex(int num_tokens, int hidden_dim, int intermediat
 int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight,
                            void* topk_indices, void* token_expert_indices, int num_tokens,
                            int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);
+
+/* Test support, no counterpart in the reference: evaluates the router's f32
+ * exponential (the f32 softmax used for f32 weights over 64-256 experts) and
+ * its f64 one on the count f32 values whose bit patterns are first_bits,
+ * first_bits + 1, ..., and folds into stats (2 device u32, zeroed by the
+ * caller): stats[0] = max(stats[0], largest distance in ulp), stats[1] +=
+ * number of inputs where the two differ. */
+int candle_moe_test_router_exp(uint32_t first_bits, uint32_t count, uint32_t* stats, void* stream);
 
 /* Token->expert grouping as fused_moe runs it internally (the reference's
  * launch_preprocessing, /root/reference/kernels/preprocessing.cuh:5-313, which

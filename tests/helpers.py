@@ -89,3 +89,60 @@ def assert_close(got: np.ndarray, want: np.ndarray, rtol: float, what: str = "",
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{got.size} elements out of tolerance (rtol={rtol}, atol={atol:.3g}); "
             f"worst at {idx}: got {got[idx]!r} want {want[idx]!r}")
+
+
+def _tile_edges(group_sizes, BM: int):
+    """Positions, in a list grouped into runs of group_sizes, of the rows at
+    the edges of every BM-row tile and of its two BM/2-row halves (the 8-wave
+    kernels' two wave rows): first and last row of each, clipped to the run."""
+    pos = []
+    start = 0
+    for n in group_sizes:
+        for t0 in range(start, start + n, BM):
+            end = min(t0 + BM, start + n)
+            for a in (t0, t0 + BM // 2):
+                if a < end:
+                    pos += [a, min(a + BM // 2, end) - 1]
+        start += n
+    return pos
+
+
+def pair_order(ri: np.ndarray, E: int):
+    """Pairs p = t*k + j grouped by expert, stable (ids >= E dropped), and
+    the per-expert counts: the grouping's order for the pair GEMMs."""
+    flat = ri.reshape(-1).astype(np.int64)
+    pairs = np.nonzero(flat < E)[0]
+    return pairs[np.argsort(flat[pairs], kind="stable")], np.bincount(flat[pairs], minlength=E)
+
+
+def set_order(ri: np.ndarray, E: int):
+    """Tokens grouped by expert set, stable: the key reads a token's ids
+    sorted ascending (ids >= E as E) as base-(E+1) digits; returns the token
+    order and the sizes of the nonempty groups in key order."""
+    T, k = ri.shape
+    ex = np.where(ri.astype(np.int64) < E, ri.astype(np.int64), E)
+    digits = np.sort(ex, axis=1, kind="stable")
+    key = np.zeros(T, dtype=np.int64)
+    for j in range(k):
+        key = key * (E + 1) + digits[:, j]
+    torder = np.argsort(key, kind="stable")
+    _, kcounts = np.unique(key[torder], return_counts=True)
+    return torder, kcounts
+
+
+def tile_covering_rows(ri: np.ndarray, E: int, BM: int, path: str) -> list:
+    """Tokens whose rows sit at the first and last row of every row tile (and
+    tile half) of the grouped GEMMs fused_moe runs on this routing, from the
+    grouping's own order (a stable counting sort, as the oracle's
+    om_preprocess): pairs p = t*k + j grouped by expert (gate/up / fc1, and
+    the pair path's down / fc2); on the expert-set path also tokens grouped by
+    their sorted expert set (the down / fc2 GEMM). Every output column of such
+    a row is checked, so every (row tile, column tile) of every launch, K-split
+    tiles included, is covered by a checked row."""
+    k = ri.shape[1]
+    order, counts = pair_order(ri, E)
+    toks = set((order[_tile_edges(counts, BM)] // k).tolist())
+    if path == "expert-set":
+        torder, kcounts = set_order(ri, E)
+        toks |= set(torder[_tile_edges(kcounts, BM)].tolist())
+    return sorted(toks)

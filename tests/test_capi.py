@@ -341,3 +341,42 @@ def test_fp8_entry_points_reject_without_launch():
     assert L.candle_moe_quantize_fp8(None, 1, 0, 16, 16, 1, None, None, None) == cm.CANDLE_MOE_OK
     assert L.candle_moe_dequantize_fp8(p, None, 1, 16, 16, p, 1, None) == cm.CANDLE_MOE_ERR_INVALID
     assert L.candle_moe_dequantize_fp8(p, p, 1, -1, 16, p, 1, None) == cm.CANDLE_MOE_ERR_INVALID
+
+
+def test_fused_moe_fp8_wrapper_checks_layouts_before_the_call():
+    """fused_moe_fp8 (Python) passes raw pointers; it first checks every
+    tensor's shape, dtype, contiguity and device (CPU tensors: nothing is
+    launched, the checks raise before the C call)."""
+    import torch
+
+    T, H, I, E, k = 4, 64, 32, 8, 2
+    x = torch.zeros(T, H, dtype=torch.bfloat16)
+    out = torch.zeros(T, H, dtype=torch.bfloat16)
+    rw = torch.zeros(T, k, dtype=torch.float32)
+    ri = torch.zeros(T, k, dtype=torch.int32)
+    gq, uq, dq = (torch.zeros(E, I, H, dtype=torch.uint8), torch.zeros(E, I, H, dtype=torch.uint8),
+                  torch.zeros(E, H, I, dtype=torch.uint8))
+    gs, us, ds = torch.ones(E, I), torch.ones(E, I), torch.ones(E, H)
+
+    def call(**kw):
+        a = dict(input=x, gate_q=gq, up_q=uq, down_q=dq, gate_scale=gs, up_scale=us, down_scale=ds,
+                 routing_weights=rw, expert_indices=ri, output=out, num_experts=E, top_k=k)
+        a.update(kw)
+        with pytest.raises(cm.CandleMoeError) as ei:
+            cm.fused_moe_fp8(**a)
+        assert ei.value.code == cm.CANDLE_MOE_ERR_INVALID
+        return str(ei.value)
+
+    assert "gate_q" in call(gate_q=torch.zeros(E, H, I, dtype=torch.uint8))  # [E,H,I] passed as [E,I,H]
+    assert "down_q" in call(down_q=torch.zeros(E, I, H, dtype=torch.uint8))
+    assert "up_q" in call(up_q=torch.zeros(E, I, H, dtype=torch.int8))
+    assert "down_scale" in call(down_scale=torch.ones(E, H, dtype=torch.float16))
+    assert "up_scale" in call(up_scale=torch.ones(E, I + 1))
+    assert "contiguous" in call(gate_q=torch.zeros(E, H, I, dtype=torch.uint8).transpose(1, 2))
+    assert "expert_indices" in call(expert_indices=torch.zeros(T, k, dtype=torch.int64))
+    assert "routing_weights" in call(routing_weights=torch.zeros(T, k + 1))
+    assert "output" in call(output=torch.zeros(T, H, dtype=torch.float16))
+    assert "down_scale" in call(down_scale=None)
+    # Nomic: fc2 codes [E, H, I] in up_q with an [E, H] scale, nothing in down
+    assert "down" in call(moe_type=1, up_q=torch.zeros(E, H, I, dtype=torch.uint8), up_scale=torch.ones(E, H))
+    assert "up_q" in call(moe_type=1, down_q=None, down_scale=None)

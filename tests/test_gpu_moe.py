@@ -14,7 +14,7 @@ import pytest
 
 import candle_moe
 import oracle as O
-from helpers import RTOL, assert_close, assert_close_norm, from_dev, moe_inputs, to_dev
+from helpers import RTOL, assert_close, assert_close_norm, from_dev, moe_inputs, tile_covering_rows, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -61,9 +61,23 @@ def run_raw(x, G, U, D, rw, ri, E, k, act, moe_type, dt, out_init=None, workspac
     return from_dev(out).astype(np.float64)
 
 
+def covering_rows(T, H, I, E, k, dt, moe_type, ri, extra=()):
+    """The first and last rows of every row tile (and tile half) of the GEMMs
+    fused_moe dispatches for this routing (the path's groupings, the
+    dispatched kernel's tile height), plus extra rows."""
+    BM = candle_moe.fused_moe_tile(T, H, I, E, k, dt, moe_type)
+    path = candle_moe.fused_moe_path(T, H, I, E, k, dt, moe_type)
+    assert BM >= 32 and path in ("expert-set", "pairs", "simt"), (BM, path)
+    rows = sorted(set(tile_covering_rows(ri, E, BM, path)) | set(extra))
+    print(f"  {len(rows)} rows cover every {BM}-row tile on the {path} path", flush=True)
+    return rows
+
+
 def check_case(T, H, I, E, k, dt, moe_type, act=O.SILU, seed=0, wstd=0.02, rows=None, skew=0.0, zipf=0.0,
                api="host"):
     x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, seed, moe_type, wstd=wstd, skew_sigma=skew, zipf_s=zipf)
+    if isinstance(rows, str) and rows == "tiles":
+        rows = covering_rows(T, H, I, E, k, dt, moe_type, ri, extra=SAMPLE if T == 32768 else ())
     if api == "host":
         got = run_moe(x, G, U, D, rw, ri, E, k, act, moe_type, dt)
     else:
@@ -123,28 +137,29 @@ def test_qwen3_30b_config(T):
 
 
 # ---- the remaining (T, dtype) points of BASELINE configs 3 and 4: every row
-# at T=512, sampled rows (each output row depends only on its own token,
-# routing and the weights) at T=4096 and 32768
+# at T=512 and 4096; at T=32768 the first and last rows of every row tile of
+# every GEMM launch (each output row depends only on its own token, its
+# routing and the weights, and every column of a checked row is compared)
 @pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
 def test_nomic_config_T512_all_rows(dt):
     check_case(512, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=32)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
-def test_nomic_config_T4096_sampled(dt):
-    check_case(4096, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=33, rows=list(range(0, 4096, 37)) + [4095])
+def test_nomic_config_T4096_all_rows(dt):
+    check_case(4096, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=33)
 
 
 @pytest.mark.slow
 @pytest.mark.parametrize("dt", [O.F32, O.F16])
-def test_nomic_config_T32768_sampled(dt):
-    check_case(32768, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=34, rows=SAMPLE)
+def test_nomic_config_T32768_tile_rows(dt):
+    check_case(32768, 768, 3072, 8, 2, dt, O.NOMIC, act=O.GELU, seed=34, rows="tiles")
 
 
 @pytest.mark.slow
-def test_qwen3_config_T32768_f16_sampled():
+def test_qwen3_config_T32768_f16_tile_rows():
     assert candle_moe.fused_moe_path(32768, 4096, 1536, 8, 2, O.F16) == "expert-set"
-    check_case(32768, 4096, 1536, 8, 2, O.F16, O.QWEN3, seed=35, rows=SAMPLE)
+    check_case(32768, 4096, 1536, 8, 2, O.F16, O.QWEN3, seed=35, rows="tiles")
 
 
 def test_activations_and_odd_shapes():
@@ -243,24 +258,25 @@ def test_deterministic_k2():
     assert np.array_equal(a, b)
 
 
-# ---- full BASELINE sizes, checked on a sample of tokens (each output row
-# depends only on its own token, its routing and the weights)
+# ---- full BASELINE sizes: the first and last rows of every row tile of
+# every GEMM launch, plus a few fixed tokens (each output row depends only on
+# its own token, its routing and the weights)
 SAMPLE = [0, 1, 2, 777, 4095, 5000, 12345, 20000, 32767]
 
 
 @pytest.mark.slow
-def test_qwen3_full_size_sampled():
-    check_case(32768, 4096, 1536, 8, 2, O.BF16, O.QWEN3, seed=15, rows=SAMPLE)
+def test_qwen3_full_size_tile_rows():
+    check_case(32768, 4096, 1536, 8, 2, O.BF16, O.QWEN3, seed=15, rows="tiles")
 
 
 @pytest.mark.slow
-def test_nomic_full_size_sampled():
-    check_case(32768, 768, 3072, 8, 2, O.BF16, O.NOMIC, act=O.GELU, seed=16, rows=SAMPLE)
+def test_nomic_full_size_tile_rows():
+    check_case(32768, 768, 3072, 8, 2, O.BF16, O.NOMIC, act=O.GELU, seed=16, rows="tiles")
 
 
 @pytest.mark.slow
-def test_qwen3_30b_prefill_sampled():
-    check_case(4096, 2048, 768, 128, 8, O.BF16, O.QWEN3, seed=17, zipf=1.1, rows=[0, 1, 100, 2047, 4095])
+def test_qwen3_30b_prefill_all_rows():
+    check_case(4096, 2048, 768, 128, 8, O.BF16, O.QWEN3, seed=17, zipf=1.1)
 
 
 # ---- the two combine paths (expert-set GEMM vs pair GEMM + pair-row sums or f32 atomics) on the same inputs
@@ -579,6 +595,8 @@ ACC_CASES = [
 
 def check_accumulate(T, H, I, E, k, dt, mt, act, zipf, expect, combine, seed, rows, offset=0, workspace=False):
     x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, seed, mt, zipf_s=zipf)
+    if isinstance(rows, str) and rows == "tiles":
+        rows = covering_rows(T, H, I, E, k, dt, mt, ri, extra=SAMPLE)
     try:
         candle_moe.set_combine_policy(combine)
         path, kernel, pair_rows = expect
@@ -626,11 +644,11 @@ def test_accumulate_unaligned_output_leaves_expert_sets(offset):
 
 
 @pytest.mark.slow
-def test_accumulate_headline_shape_sampled():
+def test_accumulate_headline_shape_tile_rows():
     # Qwen3 T=32768 bf16 through the drop-in symbol: the expert-set path with
     # the 8-wave 256x256 kernel, adding into the caller's output
     check_accumulate(32768, 4096, 1536, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, ("expert-set", 7, False), 0, seed=99,
-                     rows=SAMPLE)
+                     rows="tiles")
 
 
 def test_unaligned_16bit_operands_take_the_scalar_kernel():

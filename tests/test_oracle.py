@@ -296,3 +296,31 @@ def test_router_logits_round_once_to_dtype():
     # f32 keeps it
     got = O.router_logits(x, w, O.F32)
     assert got[0, 0] == np.float32(1.0 + 2.0 ** -8)
+
+
+def test_tile_covering_rows_brute_force():
+    """The tests' restatement of the grouping's row order and tile edges
+    (tests/helpers.py) against a hand-built table on a tiny routing."""
+    from helpers import _tile_edges, pair_order, set_order, tile_covering_rows
+
+    ri = np.array([[1, 0], [0, 1], [2, 0], [1, 1], [9, 0], [0, 2], [2, 1]], dtype=np.uint32)  # E = 3, 9 dropped
+    E = 3
+    order, counts = pair_order(ri, E)
+    # pair ids by expert, ascending inside an expert
+    assert order.tolist() == [1, 2, 5, 9, 10] + [0, 3, 6, 7, 13] + [4, 11, 12]
+    assert counts.tolist() == [5, 5, 3]
+    # sets (sorted, dropped -> 3), keys base 4: t0 {0,1}=1 t1 {0,1}=1 t2 {0,2}=2 t3 {1,1}=5
+    # t4 {0,3}=3 t5 {0,2}=2 t6 {1,2}=6
+    torder, kcounts = set_order(ri, E)
+    assert torder.tolist() == [0, 1, 2, 5, 4, 3, 6]
+    assert kcounts.tolist() == [2, 2, 1, 1, 1]
+    # edges: runs of 5 with BM = 4 -> tile [0,4) halves [0,2) [2,4), tile [4,5)
+    assert sorted(set(_tile_edges([5], 4))) == [0, 1, 2, 3, 4]
+    assert sorted(set(_tile_edges([5, 3], 8))) == [0, 3, 4, 5, 7]
+    assert sorted(set(_tile_edges([10], 4))) == [0, 1, 2, 3, 4, 5, 6, 7, 8, 9]
+    assert sorted(set(_tile_edges([10], 8))) == [0, 3, 4, 7, 8, 9]
+    # BM = 8 over the pairs: edges 0,3,4 of e0 -> pairs 1,9,10; of e1 -> 0,7,13; e2 (3 rows) 0,2 -> 4,12
+    assert tile_covering_rows(ri, E, 8, "pairs") == sorted({1 // 2, 9 // 2, 10 // 2, 0, 7 // 2, 13 // 2, 2, 6})
+    # the set order adds the first and last token of each set group
+    assert set(tile_covering_rows(ri, E, 8, "expert-set")) == \
+        set(tile_covering_rows(ri, E, 8, "pairs")) | {0, 1, 2, 5, 4, 3, 6}

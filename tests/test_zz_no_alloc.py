@@ -30,10 +30,14 @@ def _call(fn, x, G, U, D, rw, ri, E, k, act, mt, dt, init):
     return out
 
 
-# (T, H, I, E, k, dtype, moe_type, act): a prefill batch on the pair-row path,
-# then decode batches on the 32-row kernels with K splits (split-K counters and
-# the f32 accumulator live in the shared array), each smaller than the last
+# (T, H, I, E, k, dtype, moe_type, act): batches of more than 2048 pairs (the
+# multi-workgroup grouping, whose launches must not depend on what an earlier
+# call left in the shared array), a prefill batch on the pair-row path, then
+# decode batches on the 32-row kernels with K splits (split-K counters and the
+# f32 accumulator live in the shared array), each smaller than the last
 SEQUENCE = [
+    (2560, 768, 1024, 8, 2, O.F16, O.NOMIC, O.GELU),
+    (1536, 1024, 512, 8, 2, O.BF16, O.QWEN3, O.SILU),
     (512, 1024, 512, 8, 2, O.BF16, O.QWEN3, O.SILU),
     (64, 4096, 1536, 8, 2, O.BF16, O.QWEN3, O.SILU),
     (8, 4096, 1536, 8, 2, O.BF16, O.QWEN3, O.SILU),
