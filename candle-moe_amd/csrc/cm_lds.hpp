@@ -155,9 +155,11 @@ __device__ __forceinline__ u32x4 fp8x8_to(const u32x2& v) {
 // (it runs the epilogue, once per tile), the others return false. The splits
 // may run on different XCDs, whose L2s are not coherent with each other. The
 // ordering is the memory model's: every thread's partial stores precede the
-// workgroup barrier, which precedes thread 0's acquire-release increment at
-// agent scope; the last split's increment reads every earlier one (one
-// release sequence), and its partial loads follow it after a second barrier.
+// workgroup barrier, which precedes thread 0's release increment at agent
+// scope; the last split's increment reads every earlier one (one release
+// sequence), and its acquire fence (the last split only: an acquire
+// invalidates the XCD's L2 under every other workgroup there) precedes its
+// partial loads, which follow after a second barrier.
 // The partials are also written and read with device-coherent buffer
 // accesses (cache policy sc1: written through to, and read from, the level
 // shared by all XCDs). The accesses are compiler builtins, not inline asm:
@@ -187,8 +189,10 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x16 (&acc)[MB
         __builtin_amdgcn_raw_buffer_store_b128(v, pr, mine + q * 1024, 0, kCachePolicyDevice);
     }
     __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(a.counters + ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    if (threadIdx.x == 0) {
+        s_last = __hip_atomic_fetch_add(a.counters + ctr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+        if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     __syncthreads();
     if (!s_last) return false;
     // split 0 replaces the registers, the others add in split order

@@ -503,31 +503,34 @@ __device__ void one_launch_body(const GroupJob& j, int blk, int32_t* s_mem, int3
     __shared__ int s_ok;
     hist_body<TOK, K, true>(j, blk, s_mem);
     // Publication: every thread's count stores precede the barrier, the
-    // barrier precedes thread 0's release increment (agent scope), and a
-    // workgroup whose acquire poll reads the job's total synchronises with
-    // every increment before it (the increments form one release sequence),
-    // so its reads of the count table after the next barrier see every
-    // block's counts.
+    // barrier precedes thread 0's release increment (agent scope). The poll
+    // is relaxed; once it reads the job's total, one acquire fence makes the
+    // workgroup synchronise with every increment before it (the increments
+    // form one release sequence), so its reads of the count table after the
+    // next barrier see every block's counts. (An acquire on every poll would
+    // invalidate the XCD's L2 once per poll.)
     __syncthreads();
     if (threadIdx.x == 0) {
         __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         int ok = 0;
         if (spin >= 0) {
             for (int it = 0;; ++it) {
-                ok = __hip_atomic_load(sync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= j.nb;
+                ok = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= j.nb;
                 if (ok || it >= spin) break;
                 __builtin_amdgcn_s_sleep(2);
             }
         }
+        if (ok) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         s_ok = ok;
     }
     __syncthreads();
     scatter_body<TOK, K>(j, blk, s_mem, s_ok ? kCountsCoherent : kCountsRecount);
     if (threadIdx.x == 0) {
-        // (acquire-release: the last one out resets the counters after every
-        // other workgroup's poll of sync[0])
-        const int out = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        // (release, and an acquire fence in the last one out: it resets the
+        // counters after every other workgroup's poll of sync[0])
+        const int out = __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         if (out == j.nb - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

@@ -174,12 +174,15 @@ __global__ __launch_bounds__(256, 2) void moe_f32_gemm(GemmArgs a) {
                              __float_as_uint(flat[4 * q + 2]), __float_as_uint(flat[4 * q + 3])};
             __builtin_amdgcn_raw_buffer_store_b128(v, pr, mine + q * 4096u, 0, kCachePolicyDevice);
         }
-        // stores -> barrier -> acquire-release increment at agent scope (as
-        // splitk_fixup): the last split's partial loads see every split's stores
+        // stores -> barrier -> release increment at agent scope, and an
+        // acquire fence in the last split (as splitk_fixup): its partial
+        // loads see every split's stores
         __syncthreads();
-        if (tid == 0)
-            s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
                      nsplit - 1;
+            if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
         __syncthreads();
         if (!s_last) return;
         for (int s2 = 0; s2 < nsplit; ++s2) {
