@@ -464,9 +464,12 @@ def set_grouping_mode(mode: int) -> None:
 TILE_AUTO, TILE_128, TILE_LDS_128, TILE_W8, TILE_ROWS32, TILE_128x256_OCC2, TILE_F32_ROWS32, TILE_F32_128 = \
     0, 1, 5, 7, 12, 14, 15, 16
 TILE_CODES = (TILE_AUTO, TILE_128, TILE_LDS_128, TILE_W8, TILE_ROWS32, TILE_128x256_OCC2, TILE_F32_ROWS32, TILE_F32_128)
-_TILE_ROWS = {0: 64, 1: 128, 5: 128, 7: 256, 12: 32, 14: 128, 15: 32, 16: 128}
+_TILE_ROWS = {0: 64, 1: 128, 5: 128, 7: 256, 12: 32, 14: 128, 15: 32, 16: 128, 18: 16}
 # fp8 weights only (fused_moe_fp8): the register-operand decode kernel
 TILE_W8_GEMV = 17
+# 16-bit decode kernels (no grouping launch, weights straight into registers;
+# up to 1024 pairs): automatic for a few rows per touched expert
+TILE_DEC_GEMV = 18
 
 
 def set_tile_policy(policy: int) -> None:

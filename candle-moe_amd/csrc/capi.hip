@@ -258,6 +258,19 @@ static Layout make_layout(const Problem& p) {
     return L;
 }
 
+// The decode kernels (kDecGemv) group the pairs in LDS (at most
+// kDecMaxPairs of them, experts below kDecMaxE), address operands with 32-bit
+// buffer offsets and load 16-byte chunks (hidden and intermediate sizes
+// multiples of 8, 16-byte aligned operands: p.mfma).
+// (Their waves' K ranges are whole rounds of 4 steps of 32, which may run
+// up to 512 past K: the weight offsets stay below 2^31 with that margin.)
+static bool dec_gemv_fits(const Problem& p) {
+    const long long lim = 0x7fffff00LL;
+    return p.mfma && p.P <= kDecMaxPairs && p.E <= kDecMaxE && (long long)p.T * p.H * 2 < lim &&
+           p.P * p.I * 2 < lim && p.P * p.H * 2 < lim && (long long)(p.H + 1024) * p.I * 2 < lim &&
+           (long long)(p.I + 1024) * p.H * 2 < lim;
+}
+
 // aligned16: input and weights start on 16-byte boundaries (the MFMA and f32
 // tiled kernels read them with 16-byte loads; otherwise the scalar kernel
 // runs). out16: so does the output (the expert-set down GEMM stores straight
@@ -328,11 +341,13 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             p.cfg = g_tile_policy;
     } else if (p.mfma && !policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
-        if (P <= 32 * touched) p.cfg = kLdsRows32;
+        if (P <= 32 * touched) p.cfg = dec_gemv_fits(p) ? kDecGemv : kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
         else if (H <= 2048 && P < 1024 * touched && (long long)cdiv(H, 256) * est_tiles(128) >= 512)
             p.cfg = kLds128x256o2;
     }
+    // (a forced decode kernel on sizes it does not take: the 32-row kernel)
+    if (p.cfg == kDecGemv && !dec_gemv_fits(p)) p.cfg = kLdsRows32;
     // the LDS-DMA kernels address operands with 32-bit buffer offsets
     if (is_lds_cfg(p.cfg)) {
         const long long es = 2;
@@ -371,8 +386,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             // Nomic T=12288 / 32768 pairs 377 / 859 against 390 / 899 us.
             const bool rows_ok = p.mfma && is_lds_cfg(p.cfg) && p.dtype != kF32;
             const bool big_rows = (double)P * H * 2.0 >= (double)kSetMinRowBytes;
-            p.set_path = g_combine_policy == 2 ||
-                         (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets && (!rows_ok || big_rows));
+            p.set_path = p.cfg != kDecGemv &&
+                         (g_combine_policy == 2 ||
+                          (p.cfg != kLdsRows32 && (double)T >= fill * p.BM * sets && (!rows_ok || big_rows)));
         }
     }
     // K splits for the 32-row (decode) GEMMs and the f32 kernels, whose output
@@ -397,8 +413,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // Qwen3-30B-A3B shapes). Deterministic for every k. Not for the 32-row
     // decode kernels, whose few atomics cost less than the k-row pass
     // (Qwen3-30B-A3B T=16: 90 against 94 us).
-    p.rows_path = !p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 && p.cfg != kW8Gemv &&
-                  (double)P * H * 2.0 <= kRowsMaxBytes;
+    p.rows_path = p.cfg == kDecGemv ||
+                  (!p.set_path && p.lds_family && p.dtype != kF32 && p.cfg != kLdsRows32 && p.cfg != kW8Gemv &&
+                   (double)P * H * 2.0 <= kRowsMaxBytes);
     p.n_tiles1 = cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, p.cfg));
     // Decode fc1 (Nomic) likewise on 128-column tiles where the 256-column
     // ones would split K: T=16 / 64 16.8 -> 13.4, 15.2 -> 12.9 us. (The
@@ -468,6 +485,76 @@ struct Fp8Weights {
     const float* down_scale;
 };
 
+// Decode path (kDecGemv): gate/up (fc1) into inter [P, I] by pair, down
+// (fc2) into the pair rows [P, H], then each token's k rows summed in slot
+// order; the GEMM kernels group the pairs themselves (no grouping launch).
+// Columns per lane: the widest block that still gives every CU a workgroup.
+// [K,N] weights (trans): 8 or 4 columns (16 or 8-byte loads; 4-byte loads
+// ran the Qwen3 T=8 gate/up at 78 against 46 us); [N,K] weights (Nomic fc2,
+// 16-byte loads whatever the block): 8, 4 or 2 (T=16 fc2 22.3 -> 15.4 us
+// with 2).
+static int dec_cpl(long long groups, int N, bool trans) {
+    const int narrowest = trans ? 4 : 2;
+    for (int c = 8; c > narrowest; c /= 2)
+        if (groups * cdiv(N, 16 * c) >= 256) return c;
+    return narrowest;
+}
+static int run_moe_dec(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
+                       const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, const Layout& L,
+                       hipStream_t s) {
+    const bool qwen3 = p.moe_type == kQwen3;
+    void* inter = ws + L.inter;
+    void* rows = ws + L.acc;
+    DecArgs d = {};
+    d.A = x;
+    d.B0 = gate;
+    d.B1 = up;
+    d.C = inter;
+    d.idx = idx;
+    d.routing_w = rw;
+    d.P = (int)p.P;
+    d.E = p.E;
+    d.K = p.H;
+    d.N = p.I;
+    d.k_top = p.k;
+    d.act = p.act;
+    d.strideB = (long long)p.H * p.I;
+    d.ldb = p.I;
+    d.a_bytes = (long long)p.T * p.H * 2;
+    d.max_groups = (int)std::min<long long>(p.P, p.E);
+    d.rows_max = (int)std::min<long long>(p.P, p.T);
+    d.cpl = dec_cpl(d.max_groups, p.I, true);
+    d.nblk = cdiv(p.I, 16 * d.cpl);
+    hipError_t e;
+    {
+        ProfScope ps(kSlotGemm1, s);
+        e = launch_dec_gemv(qwen3 ? kGateUp : kFc1, p.dtype, d, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "fused_moe decode gate/up GEMM");
+    DecArgs d2 = d;
+    d2.A = inter;
+    d2.B0 = qwen3 ? down : up;
+    d2.B1 = nullptr;
+    d2.C = rows;
+    d2.K = p.I;
+    d2.N = p.H;
+    d2.ldb = qwen3 ? p.H : p.I;  // down [E][I][H]; Nomic fc2 (up) [E][H][I]
+    d2.a_bytes = p.P * p.I * 2;
+    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3);
+    d2.nblk = cdiv(p.H, 16 * d2.cpl);
+    {
+        ProfScope ps(kSlotGemm2, s);
+        e = launch_dec_gemv(qwen3 ? kDownRows : kFc2Rows, p.dtype, d2, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "fused_moe decode down GEMM");
+    {
+        ProfScope ps(kSlotFinal, s);
+        e = launch_pair_rows_sum(out, p.dtype, rows, idx, p.E, p.T, p.k, p.H, overwrite, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "fused_moe decode row sums");
+    return CANDLE_MOE_OK;
+}
+
 // sync_zero: the workspace's grouping counters (Layout::sync) are zero
 // (library-owned workspaces: cleared at allocation, left zero by every
 // launch), which allows the one-launch grouping.
@@ -511,6 +598,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         tb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles2);
         pair_dest = reinterpret_cast<int32_t*>(ws + L.pair_dest);
     }
+    if (p.cfg == kDecGemv) return run_moe_dec(p, x, gate, up, down, rw, idx, out, overwrite, ws, L, s);
     {
         // pairs by expert and, on the expert-set path, tokens by expert set
         const GroupJob pj = pair_grouping_job(idx, p.P, p.E, p.BM, gb);
@@ -1070,7 +1158,7 @@ int candle_moe_set_grouping_mode(int mode) {
 int candle_moe_set_tile_policy(int policy) {
     if (policy < 0 || policy >= cm::kNumTileCfgs || !cm::is_shipped_cfg(policy))
         return cm::set_error(CANDLE_MOE_ERR_INVALID,
-                             "tile policy must be one of 0 (auto), 1, 5, 7, 12, 14, 15, 16, 17 (got %d)", policy);
+                             "tile policy must be one of 0 (auto), 1, 5, 7, 12, 14, 15, 16, 17, 18 (got %d)", policy);
     cm::g_tile_policy = policy;
     return CANDLE_MOE_OK;
 }

@@ -150,17 +150,22 @@ constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter s
 //   kF32Tile128 (128x128).
 // The grouping's tile table must be built with the kernel's row tile,
 // tile_rows().
+// kDecGemv (16-bit weights, moe_gemv_dec.hip): decode GEMMs that group the
+//   pairs themselves (no grouping launch), load weights straight into
+//   registers and split K only across the waves of a workgroup; the down /
+//   fc2 GEMM stores pair rows that the k-row sum adds up.
 enum TileCfg : int {
     kTileSimt = 0, kTile128 = 1, kLds128 = 5, kLds256w8 = 7, kLdsRows32 = 12, kLds128x256o2 = 14,
-    kF32Rows32 = 15, kF32Tile128 = 16, kW8Gemv = 17
+    kF32Rows32 = 15, kF32Tile128 = 16, kW8Gemv = 17, kDecGemv = 18
 };
-constexpr int kNumTileCfgs = 18;  // codes are < kNumTileCfgs
+constexpr int kNumTileCfgs = 19;  // codes are < kNumTileCfgs
 inline bool is_shipped_cfg(int cfg) {
     return cfg == kTileSimt || cfg == kTile128 || cfg == kLds128 || cfg == kLds256w8 || cfg == kLdsRows32 ||
-           cfg == kLds128x256o2 || cfg == kF32Rows32 || cfg == kF32Tile128 || cfg == kW8Gemv;
+           cfg == kLds128x256o2 || cfg == kF32Rows32 || cfg == kF32Tile128 || cfg == kW8Gemv || cfg == kDecGemv;
 }
 inline bool is_f32_cfg(int cfg) { return cfg == kF32Rows32 || cfg == kF32Tile128; }
 inline int tile_rows(int cfg) {
+    if (cfg == kDecGemv) return 16;
     if (cfg == kLdsRows32 || cfg == kF32Rows32 || cfg == kW8Gemv) return 32;
     if (cfg == kTileSimt) return 64;
     if (cfg == kLds256w8) return 256;
@@ -218,6 +223,32 @@ hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, h
 // f32 atomics for kDown / kFc2)
 hipError_t launch_w8_gemv(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
+
+// Decode GEMMs over 16-bit weights in the API layout (moe_gemv_dec.hip).
+// Every workgroup groups the P pairs itself (P <= kDecMaxPairs, E <=
+// kDecMaxE) and takes the u-th touched expert, u = blockIdx / nblk, and
+// column block blockIdx % nblk of 16 * cpl output columns; its waves split
+// K. Modes: kGateUp, kFc1 (inter [P, N] by pair), kDownRows, kFc2Rows (rows
+// [P, N] = dtype(w_p * ...), summed per token by launch_pair_rows_sum).
+constexpr int kDecMaxPairs = 1024;
+constexpr int kDecMaxE = 4096;
+struct DecArgs {
+    const void* A;            // x [T, K] (kGateUp / kFc1) or inter [P, K] (kDownRows / kFc2Rows)
+    const void* B0;           // gate / fc1 / down / fc2 weights, expert-major
+    const void* B1;           // up weights (kGateUp)
+    void* C;                  // inter or rows [P, N] (dtype)
+    const uint32_t* idx;      // [P] expert of pair p (>= E: dropped)
+    const float* routing_w;   // [P]
+    int P, E, K, N, k_top, act;
+    long long strideB;        // elements per expert matrix
+    int ldb;                  // row pitch of B: N for [K,N] weights, K for [N,K] (kFc2Rows)
+    long long a_bytes;        // bytes of A (< 2^31)
+    int nblk;                 // column blocks of 16 * cpl columns
+    int max_groups;           // touched experts at most (grid = max_groups * nblk)
+    int rows_max;             // > 16: row chunks of 32 (two MFMA row blocks), else 16
+    int cpl;                  // columns per lane: 4 or 8
+};
+hipError_t launch_dec_gemv(int mode, int dtype, const DecArgs& a, hipStream_t stream);
 
 
 // fp8 weight preparation (fp8.hip): quantize [E][K][N] (kn) or [E][N][K]

@@ -164,8 +164,13 @@ int candle_moe_set_combine_policy(int policy);
  * 1 = register-staged MFMA kernel, 128x128 block tile (taken by default only
  *     when an operand exceeds the 2 GiB range of the LDS-DMA kernels);
  * LDS-DMA MFMA kernels: 5 = 128x128, 7 = 256x256 (8 waves),
- * 12 = 32x256 (default when experts get <= 32 rows on average),
- * 14 = 128x256 (BK 32, two workgroups per CU). By default 5 is taken for
+ * 12 = 32x256 (for <= 32 rows per expert on average where 18 does not apply),
+ * 14 = 128x256 (BK 32, two workgroups per CU);
+ * 18 = the decode kernels (f16 / bf16, at most 1024 pairs and 4096
+ *     experts): no grouping launch (each workgroup groups the pairs in LDS),
+ *     weights loaded straight into registers and transposed there, K split
+ *     across the waves of a workgroup only; default for <= 32 rows per
+ *     expert on average. By default 5 is taken for
  * <= 128 rows per expert where the 256x256 tile would give few workgroups,
  * 14 for < 1024 rows per expert with hidden_dim <= 2048 when the down GEMM
  * has at least two 128x256 tiles per CU, else 7.

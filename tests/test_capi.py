@@ -184,8 +184,9 @@ def test_moe_status_symbol_rejects_without_launch():
     # Nomic (H 768, moe_type 1): the down GEMM's 3 column tiles never fill the
     # CUs twice on the two-per-CU tile; few rows per expert take the 128x128
     # tile, the rest the 256x256 tile; its pair rows (T*k*H 16-bit values)
-    # stay below 256 MiB, so the pair path with pair rows throughout
-    (16, 768, 3072, 8, 2, 1, "pairs", 12, False),
+    # stay below 256 MiB, so the pair path with pair rows throughout; decode
+    # batches (<= 32 rows per expert) the decode kernels (18, pair rows)
+    (16, 768, 3072, 8, 2, 1, "pairs", 18, True),
     (512, 768, 3072, 8, 2, 1, "pairs", 5, True),
     (1024, 768, 3072, 8, 2, 1, "pairs", 7, True),
     (4096, 768, 3072, 8, 2, 1, "pairs", 7, True),
@@ -193,13 +194,16 @@ def test_moe_status_symbol_rejects_without_launch():
     (32768, 768, 3072, 8, 2, 1, "pairs", 7, True),
     # Qwen3-30B-A3B (H 2048, 128 experts): two-per-CU 128x256 tile below 1024
     # rows per expert; (E+1)^k keys too many for the expert-set path
+    (1, 2048, 768, 128, 8, 0, "pairs", 18, True),
+    (16, 2048, 768, 128, 8, 0, "pairs", 18, True),
     (1024, 2048, 768, 128, 8, 0, "pairs", 14, True),
     (4096, 2048, 768, 128, 8, 0, "pairs", 14, True),
     (16384, 2048, 768, 128, 8, 0, "pairs", 7, True),
     # pair rows beyond 2 GiB: f32 atomics into the [T, H] accumulator instead
     (131072, 2048, 768, 128, 8, 0, "pairs", 7, False),
     # Qwen3 (H 4096): expert sets once the pair rows reach 256 MiB (T >= 16384)
-    (8, 4096, 1536, 8, 2, 0, "pairs", 12, False),
+    (8, 4096, 1536, 8, 2, 0, "pairs", 18, True),
+    (64, 4096, 1536, 8, 2, 0, "pairs", 18, True),
     (512, 4096, 1536, 8, 2, 0, "pairs", 5, True),
     (4096, 4096, 1536, 8, 2, 0, "pairs", 7, True),
     (8192, 4096, 1536, 8, 2, 0, "pairs", 7, True),
@@ -217,10 +221,10 @@ def test_default_path_and_kernel(T, H, I, E, k, mt, path, kernel, rows):
 
 
 def test_tile_policy_accepts_only_shipped_kernels():
-    for code in cm.TILE_CODES + (cm.TILE_W8_GEMV,):
+    for code in cm.TILE_CODES + (cm.TILE_W8_GEMV, cm.TILE_DEC_GEMV):
         cm.set_tile_policy(code)
     cm.set_tile_policy(0)
-    for code in (2, 3, 4, 6, 8, 9, 10, 11, 13, 18, -1):
+    for code in (2, 3, 4, 6, 8, 9, 10, 11, 13, 19, -1):
         with pytest.raises(cm.CandleMoeError) as e:
             cm.set_tile_policy(code)
         assert e.value.code == cm.CANDLE_MOE_ERR_INVALID
