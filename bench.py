@@ -58,15 +58,18 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-sample", type=int, default=32768,
                     help="tokens in the CPU-baseline sample (0 = skip; default: the whole batch)")
-    ap.add_argument("--tile", type=int, default=0, choices=[0, 1, 5, 7, 12, 14, 15, 16, 17],
+    ap.add_argument("--tile", type=int, default=0, choices=[0, 1, 5, 7, 12, 14, 15, 16, 17, 18],
                     help="GEMM kernel: 0 auto, 1 register-staged 128x128, 5 LDS-DMA 128x128, 7 LDS-DMA 256x256 "
                          "8 waves, 12 32-row (decode), 14 128x256 two workgroups per CU, 15/16 f32 32-row / 128-row, "
-                         "17 fp8 register-operand decode kernel (--workload fp8)")
+                         "17 fp8 register-operand decode kernel (--workload fp8), 18 16-bit decode kernels")
     ap.add_argument("--combine", type=int, default=0, choices=[0, 1, 2], help="0 auto, 1 pairs, 2 expert sets")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
     ap.add_argument("--no-router-shapes", dest="router_shapes", action="store_false",
                     help="skip the topk-softmax config-2 shapes reported next to the MoE step")
+    ap.add_argument("--no-decode", dest="decode", action="store_false",
+                    help="skip the decode steps (router + forward at small T, graph-replayed) reported next to the "
+                         "headline step")
     ap.add_argument("--no-fp8-decode", dest="fp8_decode", action="store_false",
                     help="skip the decode GEMM timings with bf16 against fp8 expert weights")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -217,6 +220,7 @@ def main():
     # fused_moe symbol adding into it, ffi.rs:35), timed the same way
     dropin = bench_dropin(torch, L, x, gate, up, down, topk_w, topk_i, wl, act, args)
     router = bench_router_shapes(torch, cm, dev, args) if args.router_shapes else None
+    decode = bench_decode(torch, cm, dev, args) if args.decode else None
     fp8 = bench_fp8_decode(torch, cm, dev, args) if args.fp8_decode else None
 
     c = 6 if qwen3 else 4
@@ -263,6 +267,7 @@ def main():
         "graph_ms_per_step": round(graph_ms, 4) if graph_ms else None,
         "dropin_fused_moe": dropin,
         "topk_softmax_config2": router,
+        "decode": decode,
         "fp8_decode": fp8,
         "kernels_note": "HIP-event averages per launch: gemm_gate_up from the timed steps (the only kernel "
                         "bracketed there), the others from an untimed pass of up to 10 steps with every "
@@ -419,6 +424,91 @@ def bench_router_shapes(torch, cm, dev, args):
                      "gbs": round(nbytes / (gus * 1e-6) / 1e9, 1) if gus else None,
                      "hbm_frac": round(nbytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4) if gus else None}
         del logits
+    return res
+
+
+def bench_decode(torch, cm, dev, args):
+    """Decode steps at BASELINE's small batches: topk-softmax over [T, E]
+    logits then FusedMoE::forward, as the headline step, 20 steps in a row
+    rotating over bf16 weight copies that exceed the 256 MB last-level cache
+    (cold weights). `graph_us`: per step, the 20 steps captured once in a HIP
+    graph and replayed (every replay's outputs checked against the eager
+    ones); `eager_us`: per step between two events around the 20 launches
+    from the host. `weight_frac`: the touched experts' weight bytes at 8 TB/s
+    over graph_us (the roofline of a decode step: every touched expert's
+    weights streamed once)."""
+    res = {}
+    for wname, T in [("qwen3", 8), ("qwen3", 64), ("q30b", 1), ("q30b", 16), ("nomic", 16)]:
+        wl = WORKLOADS[wname]
+        H, I, E, k = wl["H"], wl["I"], wl["E"], wl["k"]
+        qwen3 = wl["moe_type"] == 0
+        act = {"silu": cm.Activation.Silu, "gelu": cm.Activation.Gelu, "relu": cm.Activation.Relu}[wl["act"]]
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + 100 + T)
+        nw = 3 if qwen3 else 2
+        ncopy = max(2, -(-(1024 << 20) // (nw * E * H * I * 2)))
+        x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.randn((T, E), generator=g, device=dev)
+        if wl["zipf"]:
+            ranks = torch.randperm(E, generator=torch.Generator().manual_seed(args.seed)).double() + 1
+            pz = ranks ** (-wl["zipf"])
+            logits += torch.log(pz / pz.sum()).float().to(dev)[None, :]
+        ws = []
+        for _ in range(ncopy):
+            gw = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            uw = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            dw = (torch.randn((E, I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16) if qwen3 else None
+            ws.append((gw, uw, dw))
+        tw = torch.empty((T, k), device=dev)
+        ti = torch.empty((T, k), dtype=torch.int32, device=dev)
+        tei = torch.empty((T, k), dtype=torch.int32, device=dev)
+        moe = cm.FusedMoE.new(E, k, act)
+        nsteps = 20
+
+        def steps():
+            outs = []
+            for s_ in range(nsteps):
+                cm.apply_topk_softmax_inplace(logits, tw, ti, tei)
+                gw, uw, dw = ws[s_ % ncopy]
+                outs.append(moe.forward(x, gw, uw, dw, tw, ti, wl["moe_type"]))
+            return outs
+
+        ref = steps()
+        torch.cuda.synchronize()
+        touched = int(torch.unique(ti).numel())
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        steps()
+        ev[1].record()
+        torch.cuda.synchronize()
+        eager_us = 1000.0 * ev[0].elapsed_time(ev[1]) / nsteps
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            steps()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):  # the stream whose library workspace is warm
+            gouts = steps()
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 10
+        ev[0].record()
+        for _ in range(reps):
+            graph.replay()
+        ev[1].record()
+        torch.cuda.synchronize()
+        graph_us = 1000.0 * ev[0].elapsed_time(ev[1]) / (reps * nsteps)
+        ok = all(torch.equal(a, b) for a, b in zip(gouts, ref))
+        wbytes = touched * nw * H * I * 2
+        res[f"{wname}_T{T}"] = {
+            "tokens": T, "touched_experts": touched, "weight_mb": round(wbytes / 1e6, 1),
+            "graph_us": round(graph_us, 2) if ok else None, "eager_us": round(eager_us, 2),
+            "weight_frac": round(wbytes / (PEAK_HBM_GBS * 1e9) / (graph_us * 1e-6), 4) if ok else None,
+            "kernel": cm.fused_moe_kernel(T, H, I, E, k, 1, wl["moe_type"]),
+        }
+        del ws, graph, gouts, ref
     return res
 
 

@@ -66,17 +66,20 @@ __device__ __forceinline__ u32x4 column_operand(const uint32_t (&r)[8][CPL / 2],
     return o;
 }
 
-// The touched-expert bitmap, this workgroup's expert and its pairs
-// (ascending), in LDS. Returns false when the workgroup has no expert.
+// The touched-expert bitmap and this workgroup's expert (the u-th touched
+// one), in LDS; the expert ids are kept in s_idx (-1: dropped). Returns the
+// expert, or -1 when the workgroup has none.
 template <int NT>
-__device__ __forceinline__ bool dec_group(const DecArgs& a, int u, uint32_t* s_bm, int32_t* s_rows, int* s_misc) {
+__device__ __forceinline__ int dec_expert(const DecArgs& a, int u, uint32_t* s_bm, int32_t* s_idx, int* s_misc) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwords = (a.E + 31) >> 5;
     for (int w = tid; w < nwords; w += NT) s_bm[w] = 0u;
     __syncthreads();
     for (int p = tid; p < a.P; p += NT) {
         const uint32_t e = a.idx[p];
-        if (e < (uint32_t)a.E) atomicOr(&s_bm[e >> 5], 1u << (e & 31));
+        const bool ok = e < (uint32_t)a.E;
+        s_idx[p] = ok ? (int)e : -1;
+        if (ok) atomicOr(&s_bm[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
     // wave 0: the u-th set bit (each lane two words: E <= 4096)
@@ -107,13 +110,19 @@ __device__ __forceinline__ bool dec_group(const DecArgs& a, int u, uint32_t* s_b
         }
     }
     __syncthreads();
-    const int e = s_misc[0];
-    if (e < 0) return false;
-    // the expert's pairs, ascending (stable compaction over NT-pair chunks)
+    return s_misc[0];
+}
+
+// Expert e's pairs, ascending (a stable compaction of s_idx over NT-pair
+// chunks), into s_rows; returns their number.
+template <int NT>
+__device__ __forceinline__ int dec_rows(const DecArgs& a, int e, const int32_t* s_idx, int32_t* s_rows,
+                                        int* s_misc) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int run = 0;
     for (int p0 = 0; p0 < a.P; p0 += NT) {
         const int p = p0 + tid;
-        const bool hit = p < a.P && a.idx[p] == (uint32_t)e;
+        const bool hit = p < a.P && s_idx[p] == e;
         const uint64_t m = __ballot(hit);
         if (lane == 0) s_misc[4 + wave] = __popcll(m);
         __syncthreads();
@@ -125,9 +134,7 @@ __device__ __forceinline__ bool dec_group(const DecArgs& a, int u, uint32_t* s_b
         run = total;
         __syncthreads();
     }
-    if (tid == 0) s_misc[1] = run;
-    __syncthreads();
-    return true;
+    return run;
 }
 
 template <int DT, int MODE, int RB, int CPL>
@@ -146,13 +153,14 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     static_assert(!TRANS || NB == CPL, "operands");
 
     __shared__ uint32_t s_bm[kDecMaxE / 32];
+    __shared__ int32_t s_idx[kDecMaxPairs];
     __shared__ int32_t s_rows[kDecMaxPairs];
     __shared__ int s_misc[4 + kDvWaves];
     __shared__ __attribute__((aligned(16))) float s_part[NPART][RB * 16][WGC];
 
     const int u = blockIdx.x / a.nblk, cb = blockIdx.x - u * a.nblk;
-    if (!dec_group<NT>(a, u, s_bm, s_rows, s_misc)) return;
-    const int e = s_misc[0], cnt = s_misc[1];
+    const int e = dec_expert<NT>(a, u, s_bm, s_idx, s_misc);
+    if (e < 0) return;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -193,6 +201,41 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
                                         : (uint32_t)ncol[b] * ldb2 + 16u * (uint32_t)g)
                                : kOob;
 
+    // ring of steps: weight chunks (CPL 16-bit values each for [K,N], 8 for
+    // [N,K]) and the A rows. Branch-free offsets (a select or branch on the
+    // step made the compiler wait for every load in flight): K positions
+    // past K read zeros (kOob); a [K,N] k-row past K lies past the expert's
+    // matrix, which the buffer range turns into zeros as well.
+    constexpr int WDW = TRANS ? CPL / 2 : 4;  // dwords per weight load
+    uint32_t wv[kDvRing][NLD][WDW];
+    u32x4 xv[kDvRing][RB];
+    auto load_w = [&](int i, int st) {
+        const int s = s_lo + st;
+        const bool kok = s * kDvStep + 8 * g < K;  // this lane's 8 k of the step
+#pragma unroll
+        for (int t = 0; t < NLD; ++t) {
+            uint32_t o;
+            if constexpr (TRANS) o = wlane[0] + (uint32_t)(s * kDvStep + t) * ldb2;
+            else o = kok ? wlane[t] + (uint32_t)(s * kDvStep) * 2u : kOob;
+            if constexpr (WDW == 4) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) wv[i][t][d] = v[d];
+            } else if constexpr (WDW == 2) {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0);
+                wv[i][t][0] = v[0];
+                wv[i][t][1] = v[1];
+            } else {
+                wv[i][t][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, o, 0, 0);
+            }
+        }
+    };
+    // the first ring of weight steps goes out before the expert's rows are
+    // gathered (it depends on the expert only)
+#pragma unroll
+    for (int i = 0; i < kDvRing; ++i) load_w(i, i);
+    const int cnt = dec_rows<NT>(a, e, s_idx, s_rows, s_misc);
+
     for (int c0 = 0; c0 < cnt; c0 += RB * 16) {
         const int m_valid = min(RB * 16, cnt - c0);
         // A rows of this lane (row li of each row block), k 8g
@@ -209,40 +252,17 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int b = 0; b < NB; ++b) acc[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-        // ring of steps: weight chunks (CPL 16-bit values each for [K,N],
-        // 8 for [N,K]) and the A rows. Branch-free offsets (a select or
-        // branch on the step made the compiler wait for every load in
-        // flight): K positions past K read zeros (kOob); a [K,N] k-row past
-        // K lies past the expert's matrix, which the buffer range turns into
-        // zeros as well.
-        constexpr int WDW = TRANS ? CPL / 2 : 4;  // dwords per weight load
-        uint32_t wv[kDvRing][NLD][WDW];
-        u32x4 xv[kDvRing][RB];
-        auto load = [&](int i, int st) {
+        auto load_a = [&](int i, int st) {
             const int s = s_lo + st;
-            const bool kok = s * kDvStep + 8 * g < K;  // this lane's 8 k of the step
-#pragma unroll
-            for (int t = 0; t < NLD; ++t) {
-                uint32_t o;
-                if constexpr (TRANS) o = wlane[0] + (uint32_t)(s * kDvStep + t) * ldb2;
-                else o = kok ? wlane[t] + (uint32_t)(s * kDvStep) * 2u : kOob;
-                if constexpr (WDW == 4) {
-                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0);
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) wv[i][t][d] = v[d];
-                } else if constexpr (WDW == 2) {
-                    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0);
-                    wv[i][t][0] = v[0];
-                    wv[i][t][1] = v[1];
-                } else {
-                    wv[i][t][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, o, 0, 0);
-                }
-            }
+            const bool kok = s * kDvStep + 8 * g < K;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
                 xv[i][rb] = __builtin_amdgcn_raw_buffer_load_b128(
                     rx, kok ? abase[rb] + (uint32_t)(s * kDvStep) * 2u : kOob, 0, 0);
+        };
+        auto load = [&](int i, int st) {
+            load_w(i, st);
+            load_a(i, st);
         };
         auto compute = [&](int i) {
 #pragma unroll
@@ -262,14 +282,36 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
                 for (int rb = 0; rb < RB; ++rb) acc[rb][b] = mfma16<DT>(xv[i][rb], bop, acc[rb][b]);
             }
         };
-        // (per is a positive multiple of kDvRing: the last round loads nothing)
+        // per is a positive multiple of kDvRing. The first ring round is
+        // peeled: its loads went out in another order (the weights first,
+        // before the rows were known), and inside the loop the compiler would
+        // keep that round's shorter waits for every round. The last round
+        // loads nothing; a further row chunk streams the weights again.
+        if (c0 > 0) {
 #pragma unroll
-        for (int i = 0; i < kDvRing; ++i) load(i, i);
-        for (int st = 0; st + kDvRing < per; st += kDvRing) {
+            for (int i = 0; i < kDvRing; ++i) load_w(i, i);
+        }
+#pragma unroll
+        for (int i = 0; i < kDvRing; ++i) load_a(i, i);
+        // (sched_barrier: the scheduler would otherwise hoist the MFMAs of
+        // later slots above this slot's refill, waiting for data that should
+        // still be in flight)
+        if (per > kDvRing) {
 #pragma unroll
             for (int i = 0; i < kDvRing; ++i) {
                 compute(i);
-                load(i, st + i + kDvRing);
+                __builtin_amdgcn_sched_barrier(0);
+                load(i, i + kDvRing);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            for (int st = kDvRing; st + kDvRing < per; st += kDvRing) {
+#pragma unroll
+                for (int i = 0; i < kDvRing; ++i) {
+                    compute(i);
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(i, st + i + kDvRing);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
 #pragma unroll
