@@ -67,6 +67,8 @@ def parse():
                     help="also time the step captured once in a CUDA (HIP) graph and replayed (graph_ms_per_step)")
     ap.add_argument("--no-router-shapes", dest="router_shapes", action="store_false",
                     help="skip the topk-softmax config-2 shapes reported next to the MoE step")
+    ap.add_argument("--no-packed", dest="packed", action="store_false",
+                    help="skip the step on pre-packed (K-contiguous) weights reported next to the headline")
     ap.add_argument("--no-decode", dest="decode", action="store_false",
                     help="skip the decode steps (router + forward at small T, graph-replayed) reported next to the "
                          "headline step")
@@ -221,6 +223,8 @@ def main():
     dropin = bench_dropin(torch, L, x, gate, up, down, topk_w, topk_i, wl, act, args)
     router = bench_router_shapes(torch, cm, dev, args) if args.router_shapes else None
     decode = bench_decode(torch, cm, dev, args) if args.decode else None
+    packed = (bench_packed(torch, cm, dev, args, x, gate, up, down, logits, topk_w, topk_i, tok_ei, wl)
+              if args.packed and wl["dtype"] in ("bf16", "f16") else None)
     fp8 = bench_fp8_decode(torch, cm, dev, args) if args.fp8_decode else None
 
     c = 6 if qwen3 else 4
@@ -268,6 +272,7 @@ def main():
         "dropin_fused_moe": dropin,
         "topk_softmax_config2": router,
         "decode": decode,
+        "packed_weights": packed,
         "fp8_decode": fp8,
         "kernels_note": "HIP-event averages per launch: gemm_gate_up from the timed steps (the only kernel "
                         "bracketed there), the others from an untimed pass of up to 10 steps with every "
@@ -424,6 +429,82 @@ def bench_router_shapes(torch, cm, dev, args):
                      "gbs": round(nbytes / (gus * 1e-6) / 1e9, 1) if gus else None,
                      "hbm_frac": round(nbytes / (gus * 1e-6) / 1e9 / PEAK_HBM_GBS, 4) if gus else None}
         del logits
+    return res
+
+
+def bench_packed(torch, cm, dev, args, x, gate, up, down, logits, topk_w, topk_i, tok_ei, wl):
+    """The step on pre-packed weights (the opt-in K-contiguous format,
+    candle_moe_fused_moe_packed; never the headline, which runs the drop-in
+    layout) next to the same step on the API layout through the drop-in
+    fused_moe symbol: topk-softmax, a zeroed output (both add into it) and
+    the call. ms per step, the kernels' µs per launch (HIP events around
+    every launch, a separate pass) and the gate/up GEMM's TFLOP/s for each
+    layout. hipblaslt_nk: the gate/up-sized dense GEMM [T*k, H] x [H, 2I]
+    through torch.matmul (hipBLASLt) with the weight K-contiguous ([2I, H],
+    x @ W^T), the library's figure for the packed layout on this GPU."""
+    L = cm.lib()
+    T, H, I, E, k = wl["T"], wl["H"], wl["I"], wl["E"], wl["k"]
+    qwen3 = wl["moe_type"] == 0
+    act = {"silu": 0, "gelu": 1, "relu": 2}[wl["act"]]
+    dt = {"f16": 0, "bf16": 1}[wl["dtype"]]
+    gp = cm.pack_weights(gate)
+    upk = cm.pack_weights(up) if qwen3 else up
+    dp = cm.pack_weights(down) if qwen3 else None
+    out = torch.zeros((T, H), dtype=x.dtype, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    g1_flops = float(T) * k * (4 if qwen3 else 2) * H * I
+
+    def measure(call):
+        def step():
+            cm.apply_topk_softmax_inplace(logits, topk_w, topk_i, tok_ei)
+            out.zero_()
+            call()
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        nslots = L.candle_moe_profile_begin()
+        for _ in range(min(args.steps, 10)):
+            step()
+        torch.cuda.synchronize()
+        msv = (ctypes.c_double * nslots)()
+        cnt = (ctypes.c_int * nslots)()
+        cm.check(L.candle_moe_profile_end(msv, cnt, nslots))
+        kern = {L.candle_moe_profile_slot_name(s_).decode(): round(1000.0 * msv[s_] / cnt[s_], 3)
+                for s_ in range(nslots) if cnt[s_]}
+        return {"ms_per_step": round(ms, 4), "kernels_us": kern,
+                "gate_up_tflops": round(g1_flops / (kern["gemm_gate_up"] * 1e-6) / 1e12, 1)}
+
+    res = {"note": "steps include out.zero_(): both calls add into their output",
+           "packed": measure(lambda: cm.fused_moe_packed(x, gp, upk, dp, topk_w, topk_i, out, E, k, act,
+                                                         wl["moe_type"])),
+           "api_layout": measure(lambda: L.fused_moe(p(x), p(gate), p(up), p(down), p(topk_w), p(topk_i), p(out),
+                                                     T, H, I, E, k, act, wl["moe_type"], dt, stream))}
+    del gp, upk, dp, out
+    torch.cuda.empty_cache()
+    # hipBLASLt reference: [T*k, H] x [H, 2I] with the weight stored [2I, H]
+    a = torch.randn((T * k, H), device=dev).to(torch.bfloat16)
+    w = (torch.randn((2 * I if qwen3 else I, H), device=dev) * 0.02).to(torch.bfloat16)
+    for _ in range(3):
+        c = a @ w.t()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(10):
+        c = a @ w.t()
+    ev[1].record()
+    torch.cuda.synchronize()
+    us = 1000.0 * ev[0].elapsed_time(ev[1]) / 10
+    res["hipblaslt_nk"] = {"us": round(us, 1), "tflops": round(g1_flops / (us * 1e-6) / 1e12, 1),
+                           "shape": f"[{T * k},{H}] x [{H},{w.shape[0]}] (weight [{w.shape[0]},{H}])"}
+    del a, w, c
+    torch.cuda.empty_cache()
     return res
 
 

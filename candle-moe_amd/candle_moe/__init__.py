@@ -106,6 +106,10 @@ def lib() -> ctypes.CDLL:
         L.candle_moe_fused_moe_noalloc.restype = i32
         L.candle_moe_fused_moe_noalloc_scratch_bytes.argtypes = []
         L.candle_moe_fused_moe_noalloc_scratch_bytes.restype = sz
+        L.candle_moe_pack_weights.argtypes = [vp, u32, i32, i32, i32, vp, vp]
+        L.candle_moe_pack_weights.restype = i32
+        L.candle_moe_fused_moe_packed.argtypes = moe_args + [vp]
+        L.candle_moe_fused_moe_packed.restype = i32
         L.candle_moe_test_router_exp.argtypes = [u32, u32, vp, vp]
         L.candle_moe_test_router_exp.restype = i32
         L.candle_moe_quantize_fp8.argtypes = [vp, u32, i32, i32, i32, i32, vp, vp, vp]
@@ -378,6 +382,68 @@ def fused_moe_fp8(input, gate_q, up_q, down_q, gate_scale, up_scale, down_scale,
         p(input), p(gate_q), p(up_q), p(down_q), p(gate_scale), p(up_scale), p(down_scale), p(routing_weights),
         p(expert_indices), p(output), T, H, I, num_experts, top_k, activation, moe_type,
         _torch_dtype_code(input), _stream_for(input)))
+
+
+def pack_weights(weights):
+    """Pre-packed (K-contiguous) form of 16-bit expert weights
+    (candle_moe_pack_weights): weights [E, K, N] f16/bf16, contiguous, on the
+    GPU -> a new [E, N, K] tensor of the same dtype (gate/up/fc1 [E, H, I] ->
+    [E, I, H]; down [E, I, H] -> [E, H, I])."""
+    import torch
+
+    if weights.dim() != 3 or not weights.is_contiguous() or weights.dtype not in (torch.float16, torch.bfloat16):
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "pack_weights: weights must be contiguous f16/bf16 [E, K, N]")
+    E, K, N = weights.shape
+    out = torch.empty((E, N, K), dtype=weights.dtype, device=weights.device)
+    check(lib().candle_moe_pack_weights(ctypes.c_void_p(weights.data_ptr()), _torch_dtype_code(weights), E, K, N,
+                                        ctypes.c_void_p(out.data_ptr()), _stream_for(weights)))
+    return out
+
+
+def fused_moe_packed(input, gate_packed, up_packed, down_packed, routing_weights, expert_indices, output,
+                     num_experts: int, top_k: int, activation: int = 0, moe_type: int = 0) -> None:
+    """output += MoE of input over pre-packed weights
+    (candle_moe_fused_moe_packed). Qwen3 (moe_type 0): gate/up [E, I, H],
+    down [E, H, I] (pack_weights of the API layout); Nomic (moe_type 1):
+    gate = fc1 [E, I, H] packed, up = fc2 [E, H, I] as fused_moe takes it,
+    down None. input / output [T, H] f16 or bf16, routing_weights [T, k] f32,
+    expert_indices [T, k] u32/i32; every tensor contiguous, on input's device
+    and of these shapes, else CandleMoeError."""
+    import torch
+
+    def bad(msg):
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, "fused_moe_packed: " + msg)
+
+    if input.dim() != 2 or gate_packed.dim() != 3:
+        bad("input must be [T, H] and gate_packed [E, I, H]")
+    T, H = input.shape
+    E, I = num_experts, gate_packed.shape[1]
+    want = {"gate_packed": (gate_packed, (E, I, H)), "up_packed": (up_packed, (E, I, H) if moe_type == 0 else (E, H, I)),
+            "routing_weights": (routing_weights, (T, top_k)), "expert_indices": (expert_indices, (T, top_k)),
+            "output": (output, (T, H))}
+    if moe_type == 0:
+        want["down_packed"] = (down_packed, (E, H, I))
+    elif down_packed is not None:
+        bad("Nomic (moe_type 1) takes no down_packed")
+    for name, (t, shape) in want.items():
+        if t is None:
+            bad(f"{name} is missing")
+        if tuple(t.shape) != tuple(shape):
+            bad(f"{name} must be {list(shape)}, got {list(t.shape)}")
+        if not t.is_contiguous():
+            bad(f"{name} must be contiguous")
+        if t.device != input.device:
+            bad(f"{name} must be on {input.device}")
+        dts = {"routing_weights": (torch.float32,), "expert_indices": (torch.int32, torch.uint32)}.get(
+            name, (input.dtype,))
+        if t.dtype not in dts:
+            bad(f"{name} must be {' or '.join(str(d) for d in dts)}, got {t.dtype}")
+    if not input.is_contiguous():
+        bad("input must be contiguous")
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    check(lib().candle_moe_fused_moe_packed(
+        p(input), p(gate_packed), p(up_packed), p(down_packed), p(routing_weights), p(expert_indices), p(output),
+        T, H, I, num_experts, top_k, int(activation), int(moe_type), _torch_dtype_code(input), _stream_for(input)))
 
 
 def validate_topk_softmax(g: CmTensor, w: CmTensor, i: CmTensor, ei: CmTensor) -> None:

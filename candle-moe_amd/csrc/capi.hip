@@ -130,6 +130,7 @@ int topk_softmax_impl(const void* g, int gdt, void* w, int wdt, void* idx, void*
 struct Problem {
     int T, H, I, E, k, act, moe_type, dtype;
     bool mfma;
+    bool packed;  // pre-packed K-contiguous 16-bit weights (candle_moe_fused_moe_packed)
     int cfg;  // TileCfg of both GEMMs
     int BM;
     long long P;
@@ -279,7 +280,8 @@ static bool dec_gemv_fits(const Problem& p) {
 // fp8: fp8 weights (candle_moe_fused_moe_fp8): the 32-row kernel for decode
 // batches, the 8-wave 256x256 kernel beyond, on the pair path.
 static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t moe_type, uint32_t dtype,
-                         Problem& p, bool aligned16 = true, bool out16 = true, bool fp8 = false) {
+                         Problem& p, bool aligned16 = true, bool out16 = true, bool fp8 = false,
+                         bool packed = false) {
     if (T < 0) return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: num_tokens must be >= 0 (got %d)", T);
     if (H < 1 || I < 1)
         return set_error(CANDLE_MOE_ERR_INVALID, "fused_moe: hidden_dim and intermediate_dim must be >= 1 (got %d, %d)", H, I);
@@ -295,6 +297,11 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     p.T = T; p.H = H; p.I = I; p.E = E; p.k = k; p.act = act; p.moe_type = (int)moe_type; p.dtype = (int)dtype;
     p.P = P;
     p.mfma = mfma_supported(p.dtype, H, I) && mfma_supported(p.dtype, I, H) && aligned16;
+    p.packed = packed;
+    if (packed && !p.mfma)
+        return set_error(CANDLE_MOE_ERR_UNSUPPORTED,
+                         "fused_moe_packed: needs f16 or bf16, hidden_dim and intermediate_dim multiples of 8 and "
+                         "16-byte aligned tensors (got dtype %u, %d, %d)", dtype, H, I);
     // Default MFMA kernel, by rows per touched expert (measured on MI355X
     // over T = 1 .. 32768 of the Qwen3, Qwen3-30B and Nomic shapes):
     //  * at most 32 (decode): the GEMMs stream each touched expert's weights
@@ -314,8 +321,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     // least, the rows over the tile height at least.
     const long long touched = P < E ? P : E;
     auto est_tiles = [&](int bm) { return std::max<long long>((P + bm - 1) / bm, touched); };
-    // (policy kW8Gemv concerns fp8 weights only: automatic here)
-    const int policy = g_tile_policy == kW8Gemv ? 0 : g_tile_policy;
+    // (policy kW8Gemv concerns fp8 weights only: automatic here; pre-packed
+    // weights run the LDS-DMA and decode kernels only)
+    int policy = g_tile_policy == kW8Gemv ? 0 : g_tile_policy;
+    if (packed && policy && !is_lds_cfg(policy) && policy != kDecGemv) policy = 0;
     p.cfg = !p.mfma ? kTileSimt : (policy ? policy : kLds256w8);
     // f32: the tiled vector-FMA kernel (32-row tile with K splits for decode,
     // 128-row tile otherwise) wherever 16-byte loads are possible
@@ -357,6 +366,8 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             p.cfg = kTile128;
         }
     }
+    if (packed && !is_lds_cfg(p.cfg) && p.cfg != kDecGemv)
+        return set_error(CANDLE_MOE_ERR_UNSUPPORTED, "fused_moe_packed: operands beyond 2 GiB");
     p.BM = tile_rows(p.cfg);
     // Expert-set path: each distinct sorted expert set becomes one GEMM group
     // over K = k*I; worth it when the sets are few next to the tokens: on
@@ -519,11 +530,12 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d.k_top = p.k;
     d.act = p.act;
     d.strideB = (long long)p.H * p.I;
-    d.ldb = p.I;
+    d.ldb = p.packed ? p.H : p.I;
+    d.packed = p.packed ? 1 : 0;
     d.a_bytes = (long long)p.T * p.H * 2;
     d.max_groups = (int)std::min<long long>(p.P, p.E);
     d.rows_max = (int)std::min<long long>(p.P, p.T);
-    d.cpl = dec_cpl(d.max_groups, p.I, true);
+    d.cpl = dec_cpl(d.max_groups, p.I, !p.packed);
     d.nblk = cdiv(p.I, 16 * d.cpl);
     hipError_t e;
     {
@@ -538,9 +550,9 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d2.C = rows;
     d2.K = p.I;
     d2.N = p.H;
-    d2.ldb = qwen3 ? p.H : p.I;  // down [E][I][H]; Nomic fc2 (up) [E][H][I]
+    d2.ldb = (qwen3 && !p.packed) ? p.H : p.I;  // down [E][I][H] (packed [E][H][I]); Nomic fc2 (up) [E][H][I]
     d2.a_bytes = p.P * p.I * 2;
-    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3);
+    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed);
     d2.nblk = cdiv(p.H, 16 * d2.cpl);
     {
         ProfScope ps(kSlotGemm2, s);
@@ -626,7 +638,8 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g1.num_tiles = gb.num_tiles;
     g1.offsets = gb.offsets;
     g1.strideB = (long long)p.H * p.I;
-    g1.ldb = p.I;
+    g1.ldb = p.packed ? p.H : p.I;  // gate / up / fc1: [E][H][I], or packed [E][I][H]
+    g1.packed = p.packed ? 1 : 0;
     g1.K = p.H;
     g1.N = p.I;
     g1.k_top = p.k;
@@ -670,7 +683,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         g2.B1 = nullptr;
         g2.C = out;
         g2.strideB = (long long)p.I * p.H;
-        g2.ldb = qwen3 ? p.H : p.I;
+        g2.ldb = (qwen3 && !p.packed) ? p.H : p.I;  // down [E][I][H] (packed [E][H][I]); fc2 [E][H][I]
         g2.K = p.k * p.I;
         g2.N = p.H;
         g2.a_bytes = p.P * p.I * 2;
@@ -714,7 +727,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
     g2.B1 = nullptr;
     g2.C = p.rows_path ? static_cast<void*>(ws + L.acc) : static_cast<void*>(acc);
     g2.strideB = (long long)p.I * p.H;
-    g2.ldb = qwen3 ? p.H : p.I;
+    g2.ldb = (qwen3 && !p.packed) ? p.H : p.I;  // down [E][I][H] (packed [E][H][I]); fc2 [E][H][I]
     g2.K = p.I;
     g2.N = p.H;
     g2.a_bytes = p.P * p.I * (p.dtype == kF32 ? 4 : 2);
@@ -826,12 +839,12 @@ int trim_owned_workspaces() {
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
                    uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream,
-                   const Fp8Weights* f8) {
+                   const Fp8Weights* f8, bool packed) {
     clear_error();
     Problem p;
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const bool aligned16 = a16(x) && a16(gate) && a16(up) && a16(down);
-    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out), f8 != nullptr);
+    int rc = check_problem(T, H, I, E, k, act, moe_type, dtype, p, aligned16, a16(out), f8 != nullptr, packed);
     if (rc) return rc;
     rc = check_ptrs(p, x, gate, up, down, rw, idx, out);
     if (rc) return rc;
@@ -1127,6 +1140,33 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
                                                 reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k,
                                                 reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "router_topk launch");
+}
+
+int candle_moe_pack_weights(const void* weights, uint32_t dtype, int num_experts, int k_dim, int n_dim,
+                            void* packed, void* stream) {
+    cm::clear_error();
+    if (dtype > 1)
+        return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED, "pack_weights: dtype must be 0 (f16) or 1 (bf16) (got %u)",
+                             dtype);
+    if (num_experts < 0 || k_dim < 0 || n_dim < 0)
+        return cm::set_error(CANDLE_MOE_ERR_INVALID, "pack_weights: sizes must be >= 0");
+    if ((long long)num_experts * k_dim * n_dim == 0) return CANDLE_MOE_OK;
+    if (!weights || !packed) return cm::set_error(CANDLE_MOE_ERR_INVALID, "pack_weights: null tensor pointer");
+    if (k_dim > 64 * 65535 || num_experts > 65535)
+        return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED, "pack_weights: k_dim <= 4194240 and num_experts <= 65535");
+    const hipError_t e = cm::launch_pack_kn(weights, num_experts, k_dim, n_dim, packed,
+                                            reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "pack_weights launch");
+}
+
+int candle_moe_fused_moe_packed(const void* input, const void* gate_packed, const void* up_packed,
+                                const void* down_packed, const void* routing_weights, const void* expert_indices,
+                                void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+                                void* stream) {
+    return cm::fused_moe_impl(input, gate_packed, up_packed, down_packed, routing_weights, expert_indices, output,
+                              num_tokens, hidden_dim, intermediate_dim, num_experts, num_selected_experts,
+                              activation_type, moe_type, dtype, nullptr, 0, true, false, stream, nullptr, true);
 }
 
 int candle_moe_test_router_exp(uint32_t first_bits, uint32_t count, uint32_t* stats, void* stream) {

@@ -128,6 +128,9 @@ struct GemmArgs {
     // 32-row kernel, kFc1 / kDown / kFc2 with 16-bit weights: 128-column
     // tiles instead of 256 (n_tiles counts those)
     int narrow;
+    // 16-bit weights pre-packed K-contiguous ([N,K] per expert, ldb = K) for
+    // every GEMM (candle_moe_fused_moe_packed); LDS-DMA kernels only
+    int packed;
 };
 constexpr int kTailMaxSplit = 8;
 constexpr int kTailMinKTiles = 8;  // K tiles per tail split at least (shorter splits lose to the fixup)
@@ -246,7 +249,8 @@ struct DecArgs {
     int nblk;                 // column blocks of 16 * cpl columns
     int max_groups;           // touched experts at most (grid = max_groups * nblk)
     int rows_max;             // > 16: row chunks of 32 (two MFMA row blocks), else 16
-    int cpl;                  // columns per lane: 4 or 8
+    int cpl;                  // columns per lane: 2, 4 or 8
+    int packed;               // every B [N,K] (pre-packed weights, ldb = K)
 };
 hipError_t launch_dec_gemv(int mode, int dtype, const DecArgs& a, hipStream_t stream);
 
@@ -258,6 +262,8 @@ hipError_t launch_quantize_fp8(const void* w, int dtype, int E, int K, int N, in
                                hipStream_t stream);
 hipError_t launch_dequantize_fp8(const uint8_t* q, const float* scales, int E, int N, int K, void* out, int dtype,
                                  hipStream_t stream);
+// 16-bit weights [E][K][N] -> K-contiguous [E][N][K] (the pre-packed format)
+hipError_t launch_pack_kn(const void* w, int E, int K, int N, void* out, hipStream_t stream);
 
 // f32 accumulator helpers
 hipError_t launch_fill_zero_f32(float* p, long long n, hipStream_t stream);
@@ -280,6 +286,6 @@ struct Fp8Weights;
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,
                    const void* idx, void* out, int T, int H, int I, int E, int k, int act, uint32_t moe_type,
                    uint32_t dtype, void* ws, size_t ws_bytes, bool own_ws, bool overwrite, void* stream,
-                   const Fp8Weights* f8 = nullptr);
+                   const Fp8Weights* f8 = nullptr, bool packed = false);
 
 }  // namespace cm

@@ -114,4 +114,36 @@ hipError_t launch_dequantize_fp8(const uint8_t* q, const float* scales, int E, i
     return hipGetLastError();
 }
 
+// 16-bit weights [E][K][N] -> [E][N][K]: 64 x 64 tiles through LDS, read
+// along N, written along K (rows of the padded tile 66 values apart, so the
+// column reads of the write pass spread over the banks).
+__global__ __launch_bounds__(256) void pack_kn_k(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int K,
+                                                 int N) {
+    __shared__ uint16_t t[64][66];
+    const long long e = blockIdx.z;
+    const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const uint16_t* src = w + e * K * (long long)N;
+    uint16_t* dst = out + e * N * (long long)K;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i >> 6, c = i & 63;
+        const int k = k0 + r, n = n0 + c;
+        t[r][c] = (k < K && n < N) ? src[(long long)k * N + n] : (uint16_t)0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i >> 6, c = i & 63;
+        const int n = n0 + r, k = k0 + c;
+        if (n < N && k < K) dst[(long long)n * K + k] = t[c][r];
+    }
+}
+
+hipError_t launch_pack_kn(const void* w, int E, int K, int N, void* out, hipStream_t stream) {
+    if (E <= 0 || K <= 0 || N <= 0) return hipSuccess;
+    const long long gy = (K + 63) / 64;
+    if (gy > 65535 || E > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pack_kn_k, dim3((N + 63) / 64, (unsigned)gy, E), dim3(256), 0, stream,
+                       reinterpret_cast<const uint16_t*>(w), reinterpret_cast<uint16_t*>(out), K, N);
+    return hipGetLastError();
+}
+
 }  // namespace cm

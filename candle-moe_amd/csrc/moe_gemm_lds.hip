@@ -29,7 +29,8 @@ namespace cm {
 
 using namespace lds;
 
-template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, int WGM = 2, int OCC = 1, bool W8 = false>
+template <int DT, int BM, int BN, int BK, int NST, int NW, int MODE, int WGM = 2, int OCC = 1, bool W8 = false,
+          bool PK = false>
 __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     // NW waves in WGM rows: 4 in a 2x2 layout (one per SIMD), 8 in 2x4 (two
     // per SIMD, so one wave's MFMAs cover the other's LDS, DMA and VALU work),
@@ -44,6 +45,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
     constexpr bool SET = (MODE == kDownSet || MODE == kFc2Set);
     constexpr bool BNK = (MODE == kFc2 || MODE == kFc2Set || MODE == kFc2Rows);
+    // KC: 16-bit weights stored K-contiguous ([N,K] per expert): Nomic's fc2
+    // in the API layout, or every GEMM on pre-packed weights (PK)
+    constexpr bool KC = BNK || PK;
+    static_assert(!(W8 && PK), "fp8 codes are K-contiguous already");
     constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
     constexpr bool ATOMIC = (MODE == kDown || MODE == kFc2);
     constexpr bool SWAP = !ATOMIC;
@@ -74,8 +79,13 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     constexpr int SUB_INS = SUB_BYTES / (1024 * NW);  // per wave, per sub-tile
     static_assert(A_INS * 1024 * NW == A_BYTES && SUB_INS * 1024 * NW == SUB_BYTES, "DMA split");
     static_assert(!DUAL || (WN % 64) == 0, "gate/up pairs must stay inside one wave");
-    static_assert(BNK || BCH >= 8, "[K,N] tiles need >= 8 chunks per row for the swizzle");
-    static_assert(BNK || W8 || SUB_INS * NSUB == B_INS, "B tile split");
+    static_assert(KC || BCH >= 8, "[K,N] tiles need >= 8 chunks per row for the swizzle");
+    static_assert(KC || W8 || SUB_INS * NSUB == B_INS, "B tile split");
+    // K-contiguous 16-bit sub-tiles (gate / up apart for DUAL): SUBN n-rows of
+    // AROW bytes each
+    constexpr int KSUB_BYTES = SUBN * AROW;
+    constexpr int KSUB_INS = KSUB_BYTES / (1024 * NW);
+    static_assert(!KC || (KSUB_INS * 1024 * NW == KSUB_BYTES && KSUB_INS * NSUB == B_INS), "K-contiguous B split");
     constexpr int W8_SUB_BYTES = SUBN * KROW;
     constexpr int W8_SUB_INS = W8_SUB_BYTES / (1024 * NW);
     static_assert(!W8 || (!BNK && KCH == 4 && W8_SUB_INS * 1024 * NW == W8_SUB_BYTES && W8_SUB_INS * NSUB == B_INS),
@@ -174,9 +184,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
             const int n = nt * SUBN + r;
             const int kc = a_swz<KCH>(r, lane % KCH) * 16;
             b_off[i] = n < N ? (uint32_t)n * (uint32_t)a.ldb + (uint32_t)kc : kOob;
-        } else if constexpr (BNK) {
-            const int r = RPA * (NW * i + wave) + lane / ACH;
-            const int n = nt * BN + r;
+        } else if constexpr (KC) {
+            // n-row r of sub-tile i / KSUB_INS (the only one unless DUAL)
+            const int r = RPA * (NW * (i % KSUB_INS) + wave) + lane / ACH;
+            const int n = nt * SUBN + r;
             const int kc = a_swz<ACH>(r, lane % ACH) * 8;
             b_off[i] = n < N ? ((uint32_t)n * (uint32_t)a.ldb + (uint32_t)kc) * 2u : kOob;
         } else {
@@ -233,7 +244,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         // a tile that lies inside the operands in K takes the SGPR-offset path;
         // a K tail checks every lane's chunk against K
         const uint32_t sa = (uint32_t)k0 * 2u;
-        const uint32_t sb = W8 ? (uint32_t)kk : (BNK ? (uint32_t)kk * 2u : (uint32_t)kk * (uint32_t)a.ldb * 2u);
+        const uint32_t sb = W8 ? (uint32_t)kk : (KC ? (uint32_t)kk * 2u : (uint32_t)kk * (uint32_t)a.ldb * 2u);
         if (k0 + BK <= K && kk + BK <= klim) {
             // the tile lies inside the operands in K: one SGPR offset for all lanes
 #pragma unroll
@@ -246,8 +257,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                     const int sub = i / W8_SUB_INS;
                     dma16s(sub ? rB1 : rB0, sB + sub * W8_SUB_BYTES + (NW * (i % W8_SUB_INS) + wave) * 1024, b_off[i],
                            sb);
-                } else if constexpr (BNK) {
-                    dma16s(rB0, sB + (NW * i + wave) * 1024, b_off[i], sb);
+                } else if constexpr (KC) {
+                    const int sub = i / KSUB_INS;
+                    dma16s(sub ? rB1 : rB0, sB + sub * KSUB_BYTES + (NW * (i % KSUB_INS) + wave) * 1024, b_off[i], sb);
                 } else {
                     const int sub = i / SUB_INS;  // compile-time after unrolling
                     dma16s(sub ? rB1 : rB0, sB + sub * SUB_BYTES + (NW * (i % SUB_INS) + wave) * 1024, b_off[i], sb);
@@ -272,10 +284,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                     const bool in = kk + a_swz<KCH>(r, lane % KCH) * 16 < klim;
                     dma16s(sub ? rB1 : rB0, sB + sub * W8_SUB_BYTES + (NW * (i % W8_SUB_INS) + wave) * 1024,
                            in ? b_off[i] : kOob, sb);
-                } else if constexpr (BNK) {
-                    const int r = RPA * (NW * i + wave) + lane / ACH;
+                } else if constexpr (KC) {
+                    const int sub = i / KSUB_INS;
+                    const int r = RPA * (NW * (i % KSUB_INS) + wave) + lane / ACH;
                     const bool in = kk + a_swz<ACH>(r, lane % ACH) * 8 < klim;
-                    dma16s(rB0, sB + (NW * i + wave) * 1024, in ? b_off[i] : kOob, sb);
+                    dma16s(sub ? rB1 : rB0, sB + sub * KSUB_BYTES + (NW * (i % KSUB_INS) + wave) * 1024,
+                           in ? b_off[i] : kOob, sb);
                 } else {
                     const int sub = i / SUB_INS;
                     const bool in = kk + RPI * (NW * (i % SUB_INS) + wave) + lane / BCH < klim;
@@ -322,9 +336,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            if constexpr (BNK) {
-                const int r = wn * WN + nb * 32 + lr;
-                bfr[nb] = *reinterpret_cast<const u32x4*>(sB + r * AROW + a_swz<ACH>(r, c) * 16);
+            if constexpr (KC) {
+                // DUAL: block nb is gate (even) or up (odd) of logical
+                // columns wn*WN/2 + (nb/2)*32 of the tile
+                const int sub = DUAL ? (nb & 1) : 0;
+                const int r = (DUAL ? wn * (WN / 2) + (nb >> 1) * 32 : wn * WN + nb * 32) + lr;
+                bfr[nb] = *reinterpret_cast<const u32x4*>(sB + sub * KSUB_BYTES + r * AROW + a_swz<ACH>(r, c) * 16);
             } else {
                 const int p = b_tr_col[nb];
                 const int kr = kk * 16 + tr_k;  // kr & 3 == (tj >> 2); kr + 4 keeps the swizzle
@@ -374,7 +391,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
     };
     // LDS read instructions per k16 step (ds_read_b128 for A and [N,K] B,
     // two ds_read_b64_tr_b16 per [K,N] B block).
-    constexpr int DS_PER_STEP = MB + ((BNK || W8) ? NB : 2 * NB);
+    constexpr int DS_PER_STEP = MB + ((KC || W8) ? NB : 2 * NB);
     constexpr int MFMA_PER_STEP = MB * NB;
     // Pin the schedule of one region: one MFMA, then one LDS read, while
     // reads remain, then the remaining MFMAs (masks: 0x8 MFMA, 0x100 DS read).
@@ -739,7 +756,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void moe_lds_gemm(GemmArgs a) {
                                                 (GATHER || ROWS) ? pre_w : nullptr, sc0, sc1);
 }
 
-template <int DT, int MODE>
+template <int DT, int MODE, bool PK>
 hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     // one workgroup per (row tile, column tile, K split)
     // tail balance: each XCD's range plus up to tail_cus split workgroups
@@ -754,26 +771,29 @@ hipError_t launch_lds_mode(int cfg, const GemmArgs& a, hipStream_t stream) {
     } else {
         switch (cfg) {
             case kLds128:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 128, 64, 4, 4, MODE>), dim3(nwg), dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 128, 64, 4, 4, MODE, 2, 1, false, PK>), dim3(nwg), dim3(256),
+                                   0, stream, a);
                 break;
             case kLds256w8:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 8, MODE>), dim3(nwg), dim3(512), 0, stream, a);
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 256, 256, 64, 2, 8, MODE, 2, 1, false, PK>), dim3(nwg), dim3(512),
+                                   0, stream, a);
                 break;
             case kLdsRows32:
                 if constexpr (MODE == kDown || MODE == kFc2 || MODE == kFc1) {
                     if (a.narrow) {
-                        hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0,
-                                           stream, a);
+                        hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 128, 64, 4, 4, MODE, 1, 1, false, PK>), dim3(nwg),
+                                           dim3(256), 0, stream, a);
                         break;
                     }
                 }
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1>), dim3(nwg), dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 32, 256, 64, 4, 4, MODE, 1, 1, false, PK>), dim3(nwg), dim3(256),
+                                   0, stream, a);
                 break;
             // two workgroups per CU (72 KB of LDS, at most 256 VGPRs each): one
             // workgroup's barrier and DMA issue overlap the other's MFMAs
             case kLds128x256o2:
-                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 256, 32, 3, 4, MODE, 2, 2>), dim3(nwg), dim3(256), 0,
-                                   stream, a);
+                hipLaunchKernelGGL((moe_lds_gemm<DT, 128, 256, 32, 3, 4, MODE, 2, 2, false, PK>), dim3(nwg),
+                                   dim3(256), 0, stream, a);
                 break;
             default:
                 return hipErrorInvalidValue;
@@ -840,24 +860,28 @@ hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, h
     return hipErrorInvalidValue;
 }
 
-template <int DT>
+template <int DT, bool PK>
 static hipError_t launch_lds_dt(int mode, int cfg, const GemmArgs& a, hipStream_t stream) {
+    // (pre-packed weights: every B is [N,K]; Nomic's fc2 is [N,K] either
+    // way, so its modes need no packed instances)
     switch (mode) {
-        case kGateUp: return launch_lds_mode<DT, kGateUp>(cfg, a, stream);
-        case kFc1: return launch_lds_mode<DT, kFc1>(cfg, a, stream);
-        case kDown: return launch_lds_mode<DT, kDown>(cfg, a, stream);
-        case kFc2: return launch_lds_mode<DT, kFc2>(cfg, a, stream);
-        case kDownSet: return launch_lds_mode<DT, kDownSet>(cfg, a, stream);
-        case kFc2Set: return launch_lds_mode<DT, kFc2Set>(cfg, a, stream);
-        case kDownRows: return launch_lds_mode<DT, kDownRows>(cfg, a, stream);
-        case kFc2Rows: return launch_lds_mode<DT, kFc2Rows>(cfg, a, stream);
+        case kGateUp: return launch_lds_mode<DT, kGateUp, PK>(cfg, a, stream);
+        case kFc1: return launch_lds_mode<DT, kFc1, PK>(cfg, a, stream);
+        case kDown: return launch_lds_mode<DT, kDown, PK>(cfg, a, stream);
+        case kFc2: return launch_lds_mode<DT, kFc2, false>(cfg, a, stream);
+        case kDownSet: return launch_lds_mode<DT, kDownSet, PK>(cfg, a, stream);
+        case kFc2Set: return launch_lds_mode<DT, kFc2Set, false>(cfg, a, stream);
+        case kDownRows: return launch_lds_mode<DT, kDownRows, PK>(cfg, a, stream);
+        case kFc2Rows: return launch_lds_mode<DT, kFc2Rows, false>(cfg, a, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_moe_gemm_lds(int mode, int dtype, int cfg, const GemmArgs& a, hipStream_t stream) {
-    if (dtype == kBF16) return launch_lds_dt<kBF16>(mode, cfg, a, stream);
-    if (dtype == kF16) return launch_lds_dt<kF16>(mode, cfg, a, stream);
+    if (dtype == kBF16) return a.packed ? launch_lds_dt<kBF16, true>(mode, cfg, a, stream)
+                                        : launch_lds_dt<kBF16, false>(mode, cfg, a, stream);
+    if (dtype == kF16) return a.packed ? launch_lds_dt<kF16, true>(mode, cfg, a, stream)
+                                       : launch_lds_dt<kF16, false>(mode, cfg, a, stream);
     return hipErrorInvalidValue;
 }
 

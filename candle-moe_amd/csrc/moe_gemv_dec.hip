@@ -137,11 +137,13 @@ __device__ __forceinline__ int dec_rows(const DecArgs& a, int e, const int32_t* 
     return run;
 }
 
-template <int DT, int MODE, int RB, int CPL>
+template <int DT, int MODE, int RB, int CPL, bool PK>
 __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
-    constexpr bool TRANS = (MODE != kFc2Rows);  // [K,N] weights (fc2: [N,K])
+    // [K,N] weights (the API layout but Nomic's fc2); [N,K]: fc2, and every
+    // GEMM on pre-packed weights (PK)
+    constexpr bool TRANS = (MODE != kFc2Rows) && !PK;
     constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
     constexpr int NT = 64 * kDvWaves;
     constexpr int WGC = 16 * CPL;                // output columns per workgroup
@@ -381,7 +383,15 @@ hipError_t launch_cfg(const DecArgs& a, hipStream_t stream) {
     const long long nwg = (long long)a.max_groups * a.nblk;
     if (nwg > 0x7fffffffLL) return hipErrorInvalidValue;
     if (nwg <= 0) return hipSuccess;
-    hipLaunchKernelGGL((moe_dec_gemv<DT, MODE, RB, CPL>), dim3((int)nwg), dim3(64 * kDvWaves), 0, stream, a);
+    // (Nomic's fc2 is [N,K] either way: no packed instance)
+    if constexpr (MODE != kFc2Rows) {
+        if (a.packed) {
+            hipLaunchKernelGGL((moe_dec_gemv<DT, MODE, RB, CPL, true>), dim3((int)nwg), dim3(64 * kDvWaves), 0,
+                               stream, a);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((moe_dec_gemv<DT, MODE, RB, CPL, false>), dim3((int)nwg), dim3(64 * kDvWaves), 0, stream, a);
     return hipGetLastError();
 }
 

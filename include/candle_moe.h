@@ -222,6 +222,30 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
                            void* topk_indices, void* token_expert_indices, int num_tokens,
                            int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);
 
+/* Pre-packed 16-bit expert weights (opt-in; no counterpart in the reference,
+ * whose weights are used in the API layout only, src/lib.rs:273-335): every
+ * weight matrix stored K-contiguous, [E][N][K], so that the GEMMs read it
+ * without transposing (ds_read_b128 fragments instead of transposed LDS
+ * reads; whole MFMA operands straight from memory at decode sizes).
+ *   pack_weights: weights [num_experts][k_dim][n_dim] (f16 / bf16, dtype 0 /
+ *     1) -> packed [num_experts][n_dim][k_dim], out of place, on the stream.
+ *   fused_moe_packed: fused_moe over packed weights, same arguments, result
+ *     and accumulate-into-output contract:
+ *     Qwen3 (moe_type 0): gate_packed / up_packed [E][I][H] (pack of the API's
+ *       [E][H][I]), down_packed [E][H][I] (pack of [E][I][H]);
+ *     Nomic (moe_type 1): gate_packed = fc1 [E][I][H] (pack of [E][H][I]),
+ *       up_packed = fc2 [E][H][I] exactly as fused_moe takes it (already
+ *       K-contiguous), down_packed NULL.
+ *   f16 / bf16 only, hidden_dim and intermediate_dim multiples of 8, 16-byte
+ *   aligned tensors; otherwise CANDLE_MOE_ERR_UNSUPPORTED. */
+int candle_moe_pack_weights(const void* weights, uint32_t dtype, int num_experts, int k_dim, int n_dim,
+                            void* packed, void* stream);
+int candle_moe_fused_moe_packed(const void* input, const void* gate_packed, const void* up_packed,
+                                const void* down_packed, const void* routing_weights, const void* expert_indices,
+                                void* output, int num_tokens, int hidden_dim, int intermediate_dim, int num_experts,
+                                int num_selected_experts, int activation_type, uint32_t moe_type, uint32_t dtype,
+                                void* stream);
+
 /* Test support, no counterpart in the reference: evaluates the router's f32
  * exponential (the f32 softmax used for f32 weights over 64-256 experts) and
  * its f64 one on the count f32 values whose bit patterns are first_bits,
