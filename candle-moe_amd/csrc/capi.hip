@@ -1135,10 +1135,30 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
         return cm::set_error(CANDLE_MOE_ERR_INVALID, "router_topk: null tensor pointer");
     if (((uintptr_t)hidden | (uintptr_t)router_weight) & 15)
         return cm::set_error(CANDLE_MOE_ERR_UNSUPPORTED, "router_topk: hidden and router_weight must be 16-byte aligned");
-    const hipError_t e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
-                                                reinterpret_cast<uint32_t*>(topk_indices),
-                                                reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k,
-                                                reinterpret_cast<hipStream_t>(stream));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // small batches split K over workgroups, with f32 partials in the
+    // library-owned workspace of this (device, stream) (held while enqueuing,
+    // as fused_moe does)
+    const size_t need = cm::router_ws_bytes(T, H, E, (int)dtype);
+    hipError_t e = hipSuccess;
+    if (need > 0) {
+        int dev = 0;
+        e = hipGetDevice(&dev);
+        if (e != hipSuccess) return cm::hip_fail(e, "router_topk: hipGetDevice");
+        std::lock_guard<std::mutex> lk(cm::g_ws_mu);
+        cm::OwnedWs* w = cm::owned_ws_locked(dev, s, need, e);
+        if (!w)
+            return cm::set_error(CANDLE_MOE_ERR_WORKSPACE, "router_topk: hipMallocAsync(%zu) failed: %s", need,
+                                 hipGetErrorString(e));
+        e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
+                                   reinterpret_cast<uint32_t*>(topk_indices),
+                                   reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k, s,
+                                   reinterpret_cast<float*>(w->ptr), w->bytes);
+    } else {
+        e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
+                                   reinterpret_cast<uint32_t*>(topk_indices),
+                                   reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k, s);
+    }
     return e == hipSuccess ? CANDLE_MOE_OK : cm::hip_fail(e, "router_topk launch");
 }
 

@@ -8,8 +8,13 @@
 namespace cm {
 
 // ---------------------------------------------------------------- router
+// part / part_bytes: workspace of router_ws_bytes() for the K-split form of
+// small batches (router_splits() > 1); without it one workgroup per tile.
 hipError_t launch_router_topk(const void* x, const void* w, int dtype, float* wo, uint32_t* io, uint32_t* eo, int T,
-                              int H, int E, int k, hipStream_t stream);
+                              int H, int E, int k, hipStream_t stream, float* part = nullptr,
+                              size_t part_bytes = 0);
+int router_splits(int T, int H, int E, int dtype);
+size_t router_ws_bytes(int T, int H, int E, int dtype);
 hipError_t launch_topk_softmax(const void* logits, int in_dtype, void* w, int w_dtype, uint32_t* idx,
                                uint32_t* ei, int T, int E, int k, hipStream_t stream);
 // test support: the router's f32 exponential against its f64 one

@@ -731,6 +731,46 @@ static hipError_t launch_dt(const void* logits, void* w, uint32_t* idx, uint32_t
     return launch_cfg<32, 32, INDT, OUTDT>(logits, w, idx, ei, T, E, k, stream);
 }
 
+constexpr int kRouterMaxSlots = 8;  // K splits of the small-batch router at most
+// The softmax / top-k of logits given as ns f32 partial sums: logit[t][e] =
+// dtype(part[0][t][e] + part[1][t][e] + ... ) summed in slot order (the
+// K-split router), rounded once to the router's dtype as the matmul stores it.
+template <int VPT, int LPR, int DT>
+__global__ __launch_bounds__(256) void topk_partials_kernel(const float* __restrict__ part, int ns,
+                                                           void* __restrict__ wout, uint32_t* __restrict__ iout,
+                                                           uint32_t* __restrict__ eiout, int T, int E, int k,
+                                                           int aligned) {
+    const long long gtid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long row = gtid / LPR;
+    const int g = (int)(gtid % LPR);
+    const bool valid = row < T;
+    const long long r = valid ? row : (long long)T - 1;
+    const int e0 = g * VPT;
+    const bool full = aligned && (E == LPR * VPT);
+    // every slot's loads in flight together (ns <= kRouterMaxSlots), then
+    // the sums in slot order
+    float y[kRouterMaxSlots][VPT];
+#pragma unroll
+    for (int sl = 0; sl < kRouterMaxSlots; ++sl)
+        if (sl < ns) load_row_values<VPT, kF32>(part + (long long)sl * T * E, r, E, e0, full, y[sl]);
+    float x[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) x[j] = y[0][j];
+#pragma unroll
+    for (int sl = 1; sl < kRouterMaxSlots; ++sl)
+        if (sl < ns) {
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) x[j] += y[sl][j];
+        }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+        x[j] = e0 + j < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(x[j])) : -__builtin_inff();
+    constexpr bool FAST = VPT <= 8 && LPR * VPT <= 256 && LPR > 1;
+    __shared__ float s_p[FAST ? 256 / LPR : 1][FAST ? LPR * VPT : 1];
+    softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
+                                       FAST ? s_p[threadIdx.x / LPR] : nullptr);
+}
+
 // ------------------------------------------------------------------------
 // Router GEMM fused with topk-softmax: logits[t,e] = dtype(sum_h x[t,h] *
 // w[e,h]) with f32 accumulation and one rounding to the input dtype (the
@@ -880,12 +920,17 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const void* __restrict_
 // order) so that each holds whole tokens for the softmax over 32-lane groups
 // (VPT = NB experts per lane, stride 32); KH = 2 halves the rows each wave
 // ranks, whose top-k passes dominate small batches.
-template <int DT, int NB, int MT, int NST, int KH>
+// PART (small batches): the grid is token tiles x ks K splits; split s of a
+// tile runs K tiles [s*per, (s+1)*per) and stores each wave's f32 partial
+// logits (no rounding, no softmax) to part[s*KH + kh][t][e], for
+// topk_partials_kernel to sum in split order.
+template <int DT, int NB, int MT, int NST, int KH, bool PART = false>
 __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* __restrict__ xin,
                                                               const void* __restrict__ win,
                                                               float* __restrict__ wout, uint32_t* __restrict__ iout,
                                                               uint32_t* __restrict__ eiout, int T, int H, int E,
-                                                              int k) {
+                                                              int k, float* __restrict__ part = nullptr,
+                                                              int ks = 1) {
     using namespace lds;
     typedef typename Elem<DT>::storage S;
     constexpr int TM = 32 * MT;                   // tokens per workgroup
@@ -900,7 +945,8 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cb = wave % NB, kh = wave / NB;  // expert block, K part
-    const long long t0 = (long long)blockIdx.x * TM;  // < T (grid = ceil(T/TM))
+    const int split = PART ? (int)(blockIdx.x % ks) : 0;
+    const long long t0 = (long long)(PART ? blockIdx.x / ks : blockIdx.x) * TM;  // < T (grid = ceil(T/TM) x ks)
     const int rows = T - t0 < TM ? (int)(T - t0) : TM;
     const i32x4 rx = make_rsrc(reinterpret_cast<const S*>(xin) + t0 * H, (long long)rows * H * 2);
     const i32x4 rw = make_rsrc(win, (long long)E * H * 2);
@@ -922,7 +968,10 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
         off[i] = is_x[i] ? ((uint32_t)row * (uint32_t)H + 8u * c) * 2u
                          : ((uint32_t)(row - TM) * (uint32_t)H + 8u * c) * 2u;  // rows >= rows / E: past the resource
     }
-    const int nk = (H + 63) / 64;
+    const int nk_all = (H + 63) / 64;
+    const int per = (nk_all + ks - 1) / ks;
+    const int kt_lo = PART ? min(nk_all, split * per) : 0;
+    const int nk = PART ? min(nk_all, kt_lo + per) - kt_lo : nk_all;  // this split's K tiles (may be 0)
     auto issue = [&](int stage, int k0) {
         const uint32_t sl = sbase + stage * STAGE;
         const bool full = k0 + 64 <= H;
@@ -942,7 +991,7 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
     const bool dma = kh == 0;
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
-        if (dma && s < nk) issue(s, s * 64);
+        if (dma && s < nk) issue(s, (kt_lo + s) * 64);
     for (int kt = 0; kt < nk; ++kt) {
         // this wave's DMA of tile kt (NST-2 newer tiles may stay in flight),
         // then the barrier makes every wave's part visible and frees slot kt-1
@@ -954,7 +1003,7 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
         else wait_vm<0>();
         wait_lgkm0();
         block_barrier();
-        if (dma && kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt + NST - 1) * 64);
+        if (dma && kt + NST - 1 < nk) issue((kt + NST - 1) % NST, (kt_lo + kt + NST - 1) * 64);
         const char* sx = smem + (kt % NST) * STAGE;
         const char* sw = sx + TM * 128;
 #pragma unroll
@@ -970,6 +1019,20 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
                 acc[m] = mfma32<DT>(a, b, acc[m]);
             }
         }
+    }
+    if constexpr (PART) {
+        // register i of block m: token 32m + 8(i/4) + 4(l/32) + i%4, expert
+        // 32cb + l%32 (32 consecutive experts per store instruction)
+        float* dst = part + (long long)(split * KH + kh) * T * E;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const long long t = t0 + 32 * m + 8 * (i / 4) + 4 * lh + (i % 4);
+                const int e = 32 * cb + lr;
+                if (t < T && e < E) dst[t * E + e] = acc[m][i];
+            }
+        return;
     }
     // exchange through LDS (the ring is free after the barrier):
     // red[kh][m][c][i][lane]
@@ -1024,6 +1087,46 @@ __global__ __launch_bounds__(64 * NB * KH) void router_mfma_kernel(const void* _
     }
 }
 
+// Small batches (at most kRouterSplitTiles tiles of 32 tokens): K split over
+// ks workgroups per tile (aiming at ~64 workgroups, at least 2 K tiles each,
+// at most kRouterMaxSlots splits), one f32 partial per split in the caller's
+// workspace (the split's waves each cover all of its K tiles), then the
+// softmax / top-k summing them (two launches instead of one workgroup per
+// tile streaming the whole router weight).
+constexpr int kRouterSplitTiles = 8;
+int router_splits(int T, int H, int E, int dtype) {
+    if (dtype == kF32 || E <= 32 || E > 128) return 1;
+    const long long tiles = ((long long)T + 31) / 32;
+    if (tiles > kRouterSplitTiles) return 1;
+    const int nk = (H + 63) / 64;
+    int ks = (int)(64 / tiles);
+    ks = std::min(ks, std::min(kRouterMaxSlots, nk / 2));
+    return ks >= 2 ? ks : 1;
+}
+size_t router_ws_bytes(int T, int H, int E, int dtype) {
+    const int ks = router_splits(T, H, E, dtype);
+    return ks > 1 ? (size_t)ks * T * E * sizeof(float) : 0;
+}
+
+template <int DT, int NB>
+static hipError_t launch_router_split(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
+                                      int H, int E, int k, int ks, float* part, hipStream_t stream) {
+    const long long grid = ((long long)T + 31) / 32 * ks;
+    hipLaunchKernelGGL((router_mfma_kernel<DT, NB, 1, 6, 1, true>), dim3((unsigned)grid), dim3(64 * NB), 0, stream,
+                       x, w, wo, io, eo, T, H, E, k, part, ks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int aligned = ((uintptr_t)part % 16) == 0;
+    const unsigned g2 = (unsigned)cdivll((long long)T * 16, 256);
+    if (E <= 64)
+        hipLaunchKernelGGL((topk_partials_kernel<8, 8, DT>), dim3((unsigned)cdivll((long long)T * 8, 256)), dim3(256),
+                           0, stream, part, ks, wo, io, eo, T, E, k, aligned);
+    else
+        hipLaunchKernelGGL((topk_partials_kernel<8, 16, DT>), dim3(g2), dim3(256), 0, stream, part, ks, wo, io, eo,
+                           T, E, k, aligned);
+    return hipGetLastError();
+}
+
 template <int DT, int NB>
 static hipError_t launch_router_mfma(const void* x, const void* w, float* wo, uint32_t* io, uint32_t* eo, int T,
                                      int H, int E, int k, hipStream_t stream) {
@@ -1074,8 +1177,16 @@ static hipError_t launch_router_dt(const void* x, const void* w, float* wo, uint
 }
 
 hipError_t launch_router_topk(const void* x, const void* w, int dtype, float* wo, uint32_t* io, uint32_t* eo, int T,
-                              int H, int E, int k, hipStream_t stream) {
+                              int H, int E, int k, hipStream_t stream, float* part, size_t part_bytes) {
     if (T == 0) return hipSuccess;
+    const int ks = router_splits(T, H, E, dtype);
+    if (ks > 1 && part && part_bytes >= router_ws_bytes(T, H, E, dtype)) {
+        if (dtype == kBF16)
+            return E <= 64 ? launch_router_split<kBF16, 2>(x, w, wo, io, eo, T, H, E, k, ks, part, stream)
+                           : launch_router_split<kBF16, 4>(x, w, wo, io, eo, T, H, E, k, ks, part, stream);
+        return E <= 64 ? launch_router_split<kF16, 2>(x, w, wo, io, eo, T, H, E, k, ks, part, stream)
+                       : launch_router_split<kF16, 4>(x, w, wo, io, eo, T, H, E, k, ks, part, stream);
+    }
     if (dtype == kBF16) return launch_router_dt<kBF16>(x, w, wo, io, eo, T, H, E, k, stream);
     if (dtype == kF16) return launch_router_dt<kF16>(x, w, wo, io, eo, T, H, E, k, stream);
     if (dtype == kF32) return launch_router_dt<kF32>(x, w, wo, io, eo, T, H, E, k, stream);
