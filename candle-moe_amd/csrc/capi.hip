@@ -192,6 +192,7 @@ constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
 // over ~30 experts) 51.6 against 40.2. (The host cannot tell how many
 // experts a batch touches, so the bound is on the pairs.)
 constexpr long long kW8GemvPairs = 16;
+constexpr long long kW8DecPairs = 32;
 static int g_combine_policy = 0;
 // 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
@@ -345,8 +346,16 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         // staging, no K splits across workgroups), up to 32 rows per touched
         // expert the 32-row tile kernel; beyond, the 8-wave 256x256 kernel.
         // Tile policies 17, 12 and 7 force one of them.
+        // Up to kW8DecPairs pairs the decode kernels instead (the pairs
+        // grouped inside the GEMM kernels, no grouping launch; GEMM time at
+        // Qwen3 T=16 / Qwen3-30B-A3B T=1 / Nomic T=16 48.7 / 19.3 / 22.6
+        // against 53.3 / 21.8 / 27.6 us; at 128 pairs (Qwen3 T=64,
+        // Qwen3-30B-A3B T=16) 62 / 51 against 54 / 40 us: the column blocks
+        // are sized for the touched experts' upper bound, min(pairs, E)).
         p.cfg = (P <= kW8GemvPairs) ? kW8Gemv : (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
-        if (g_tile_policy == kW8Gemv || g_tile_policy == kLdsRows32 || g_tile_policy == kLds256w8)
+        if (P <= kW8DecPairs && dec_gemv_fits(p)) p.cfg = kDecGemv;
+        if (g_tile_policy == kW8Gemv || g_tile_policy == kLdsRows32 || g_tile_policy == kLds256w8 ||
+            (g_tile_policy == kDecGemv && dec_gemv_fits(p)))
             p.cfg = g_tile_policy;
     } else if (p.mfma && !policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
@@ -512,7 +521,7 @@ static int dec_cpl(long long groups, int N, bool trans) {
 }
 static int run_moe_dec(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
                        const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, const Layout& L,
-                       hipStream_t s) {
+                       hipStream_t s, const Fp8Weights* f8) {
     const bool qwen3 = p.moe_type == kQwen3;
     void* inter = ws + L.inter;
     void* rows = ws + L.acc;
@@ -530,12 +539,17 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d.k_top = p.k;
     d.act = p.act;
     d.strideB = (long long)p.H * p.I;
-    d.ldb = p.packed ? p.H : p.I;
+    d.ldb = (p.packed || f8) ? p.H : p.I;  // gate / up [E][H][I], or packed / fp8 codes [E][I][H]
     d.packed = p.packed ? 1 : 0;
+    if (f8) {
+        d.w8 = 1;
+        d.scale0 = f8->gate_scale;
+        d.scale1 = f8->up_scale;
+    }
     d.a_bytes = (long long)p.T * p.H * 2;
     d.max_groups = (int)std::min<long long>(p.P, p.E);
     d.rows_max = (int)std::min<long long>(p.P, p.T);
-    d.cpl = dec_cpl(d.max_groups, p.I, !p.packed);
+    d.cpl = dec_cpl(d.max_groups, p.I, !p.packed && !f8);
     d.nblk = cdiv(p.I, 16 * d.cpl);
     hipError_t e;
     {
@@ -550,9 +564,13 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d2.C = rows;
     d2.K = p.I;
     d2.N = p.H;
-    d2.ldb = (qwen3 && !p.packed) ? p.H : p.I;  // down [E][I][H] (packed [E][H][I]); Nomic fc2 (up) [E][H][I]
+    d2.ldb = (qwen3 && !p.packed && !f8) ? p.H : p.I;  // down [E][I][H] (packed / fp8 [E][H][I]); fc2 [E][H][I]
+    if (f8) {
+        d2.scale0 = qwen3 ? f8->down_scale : f8->up_scale;
+        d2.scale1 = nullptr;
+    }
     d2.a_bytes = p.P * p.I * 2;
-    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed);
+    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed && !f8);
     d2.nblk = cdiv(p.H, 16 * d2.cpl);
     {
         ProfScope ps(kSlotGemm2, s);
@@ -610,7 +628,7 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         tb.num_tiles = reinterpret_cast<int32_t*>(ws + L.num_tiles2);
         pair_dest = reinterpret_cast<int32_t*>(ws + L.pair_dest);
     }
-    if (p.cfg == kDecGemv) return run_moe_dec(p, x, gate, up, down, rw, idx, out, overwrite, ws, L, s);
+    if (p.cfg == kDecGemv) return run_moe_dec(p, x, gate, up, down, rw, idx, out, overwrite, ws, L, s, f8);
     {
         // pairs by expert and, on the expert-set path, tokens by expert set
         const GroupJob pj = pair_grouping_job(idx, p.P, p.E, p.BM, gb);

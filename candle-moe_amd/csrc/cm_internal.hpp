@@ -256,6 +256,9 @@ struct DecArgs {
     int rows_max;             // > 16: row chunks of 32 (two MFMA row blocks), else 16
     int cpl;                  // columns per lane: 2, 4 or 8
     int packed;               // every B [N,K] (pre-packed weights, ldb = K)
+    int w8;                   // fp8 e4m3 codes [E][N][K] (ldb = K) with f32 scales [E][N]
+    const float* scale0;      // (w8) gate / fc1 / down / fc2 column scales
+    const float* scale1;      // (w8) up column scales
 };
 hipError_t launch_dec_gemv(int mode, int dtype, const DecArgs& a, hipStream_t stream);
 

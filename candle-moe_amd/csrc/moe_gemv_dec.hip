@@ -137,13 +137,20 @@ __device__ __forceinline__ int dec_rows(const DecArgs& a, int e, const int32_t* 
     return run;
 }
 
-template <int DT, int MODE, int RB, int CPL, bool PK>
+template <int DT, int MODE, int RB, int CPL, bool PK, bool W8 = false>
 __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     constexpr bool DUAL = (MODE == kGateUp);
     constexpr bool GATHER = (MODE == kGateUp || MODE == kFc1);
-    // [K,N] weights (the API layout but Nomic's fc2); [N,K]: fc2, and every
-    // GEMM on pre-packed weights (PK)
-    constexpr bool TRANS = (MODE != kFc2Rows) && !PK;
+    // [K,N] weights (the API layout but Nomic's fc2); [N,K]: fc2, every GEMM
+    // on pre-packed weights (PK) and on fp8 codes (W8)
+    constexpr bool TRANS = (MODE != kFc2Rows) && !PK && !W8;
+    // W8: OCP fp8 e4m3 codes [E][N][K] (one byte per weight) with per-column
+    // f32 scales. A step is 64 k: a lane's 16-byte load holds k0 + 16g .. +15
+    // of its column, the operands of two MFMAs (converted exactly to DT),
+    // and the A operand holds the same k of its row in two 16-byte loads.
+    constexpr int KSTEP = W8 ? 64 : kDvStep;
+    constexpr int KG = W8 ? 16 : 8;   // k per lane group per step
+    constexpr int WB = W8 ? 1 : 2;    // bytes per weight
     constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
     constexpr int NT = 64 * kDvWaves;
     constexpr int WGC = 16 * CPL;                // output columns per workgroup
@@ -173,15 +180,15 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     const int col0 = cb * WGC;
 
     // weights of expert e (this wave's tensor): in-range loads only, zeros past
-    const char* wbase = reinterpret_cast<const char*>(tensor ? a.B1 : a.B0) + (long long)e * a.strideB * 2;
+    const char* wbase = reinterpret_cast<const char*>(tensor ? a.B1 : a.B0) + (long long)e * a.strideB * WB;
     const __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), 0, (int)(a.strideB * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wbase), 0, (int)(a.strideB * WB), 0x00020000);
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.A), 0, (int)a.a_bytes, 0x00020000);
 
     // this wave's steps: a whole number of ring rounds (steps past K load
     // zeros), so that the ring loop needs no guard
-    const int nks = (K + kDvStep - 1) / kDvStep;
+    const int nks = (K + KSTEP - 1) / KSTEP;
     const int per = ((nks + KP - 1) / KP + kDvRing - 1) / kDvRing * kDvRing;
     const int s_lo = kpart * per;
 
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     // [N,K]: column ncol[b], k 8g. A lane whose columns lie past N starts at
     // kOob. (Every offset stays below 2^32: kOob plus less than the expert's
     // 2^31 bytes.)
-    const uint32_t ldb2 = (uint32_t)a.ldb * 2u;
+    const uint32_t ldb2 = (uint32_t)a.ldb * (uint32_t)WB;  // bytes per weight row
     uint32_t wlane[TRANS ? 1 : NB];
 #pragma unroll
     for (int b = 0; b < (TRANS ? 1 : NB); ++b)
@@ -210,15 +217,15 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
     // matrix, which the buffer range turns into zeros as well.
     constexpr int WDW = TRANS ? CPL / 2 : 4;  // dwords per weight load
     uint32_t wv[kDvRing][NLD][WDW];
-    u32x4 xv[kDvRing][RB];
+    u32x4 xv[kDvRing][RB][W8 ? 2 : 1];
     auto load_w = [&](int i, int st) {
         const int s = s_lo + st;
-        const bool kok = s * kDvStep + 8 * g < K;  // this lane's 8 k of the step
+        const bool kok = s * KSTEP + KG * g < K;  // this lane's k of the step
 #pragma unroll
         for (int t = 0; t < NLD; ++t) {
             uint32_t o;
-            if constexpr (TRANS) o = wlane[0] + (uint32_t)(s * kDvStep + t) * ldb2;
-            else o = kok ? wlane[t] + (uint32_t)(s * kDvStep) * 2u : kOob;
+            if constexpr (TRANS) o = wlane[0] + (uint32_t)(s * KSTEP + t) * ldb2;
+            else o = kok ? wlane[t] + (uint32_t)(s * KSTEP * WB) : kOob;
             if constexpr (WDW == 4) {
                 const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0);
 #pragma unroll
@@ -247,7 +254,7 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
             const int m = rb * 16 + li;
             const int p = s_rows[c0 + min(m, m_valid - 1)];
             const int src = GATHER ? p / a.k_top : p;
-            abase[rb] = m < m_valid ? ((uint32_t)src * (uint32_t)K + 8u * (uint32_t)g) * 2u : kOob;
+            abase[rb] = m < m_valid ? ((uint32_t)src * (uint32_t)K + (uint32_t)(KG * g)) * 2u : kOob;
         }
         f32x4 acc[RB][NB];
 #pragma unroll
@@ -256,11 +263,13 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
             for (int b = 0; b < NB; ++b) acc[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
         auto load_a = [&](int i, int st) {
             const int s = s_lo + st;
-            const bool kok = s * kDvStep + 8 * g < K;
+            const bool kok = s * KSTEP + KG * g < K;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
-                xv[i][rb] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rx, kok ? abase[rb] + (uint32_t)(s * kDvStep) * 2u : kOob, 0, 0);
+#pragma unroll
+                for (int h = 0; h < (W8 ? 2 : 1); ++h)
+                    xv[i][rb][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rx, kok ? abase[rb] + (uint32_t)(s * KSTEP) * 2u + 16u * h : kOob, 0, 0);
         };
         auto load = [&](int i, int st) {
             load_w(i, st);
@@ -269,19 +278,30 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
         auto compute = [&](int i) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                u32x4 bop;
-                if constexpr (TRANS) {
-                    uint32_t r[8][CPL / 2];
+                if constexpr (W8) {
+                    // codes k0 + 16g .. +7 and .. +15 of column b: two operands
+                    const u32x4 wl = fp8x8_to<DT>(u32x2{wv[i][b][0], wv[i][b][1]});  // exact in DT
+                    const u32x4 wh = fp8x8_to<DT>(u32x2{wv[i][b][2], wv[i][b][3]});
 #pragma unroll
-                    for (int t = 0; t < 8; ++t)
-#pragma unroll
-                        for (int d = 0; d < CPL / 2; ++d) r[t][d] = wv[i][t][d];
-                    bop = column_operand<CPL>(r, b);
+                    for (int rb = 0; rb < RB; ++rb) {
+                        acc[rb][b] = mfma16<DT>(xv[i][rb][0], wl, acc[rb][b]);
+                        acc[rb][b] = mfma16<DT>(xv[i][rb][1], wh, acc[rb][b]);
+                    }
                 } else {
-                    bop = u32x4{wv[i][b][0], wv[i][b][1], wv[i][b][2], wv[i][b][3]};
-                }
+                    u32x4 bop;
+                    if constexpr (TRANS) {
+                        uint32_t r[8][CPL / 2];
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) acc[rb][b] = mfma16<DT>(xv[i][rb], bop, acc[rb][b]);
+                        for (int t = 0; t < 8; ++t)
+#pragma unroll
+                            for (int d = 0; d < CPL / 2; ++d) r[t][d] = wv[i][t][d];
+                        bop = column_operand<CPL>(r, b);
+                    } else {
+                        bop = u32x4{wv[i][b][0], wv[i][b][1], wv[i][b][2], wv[i][b][3]};
+                    }
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) acc[rb][b] = mfma16<DT>(xv[i][rb][0], bop, acc[rb][b]);
+                }
             }
         };
         // per is a positive multiple of kDvRing. The first ring round is
@@ -350,11 +370,15 @@ __global__ __launch_bounds__(64 * kDvWaves, 1) void moe_dec_gemv(DecArgs a) {
                         v[pt] = *reinterpret_cast<const f32x4*>(&s_part[pt][m][c8 + 4 * half]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
+                        // (fp8 weights: the column scales on the f32 sums first)
+                        const int cc = col + 4 * half + j;
+                        const float s0 = W8 ? (cc < N ? a.scale0[(long long)e * N + cc] : 0.0f) : 1.0f;
                         float y;
                         if constexpr (DUAL) {
-                            y = act_t<ACT>(v[0][j] + v[1][j]) * (v[2][j] + v[3][j]);
+                            const float s1 = W8 ? (cc < N ? a.scale1[(long long)e * N + cc] : 0.0f) : 1.0f;
+                            y = act_t<ACT>(s0 * (v[0][j] + v[1][j])) * (s1 * (v[2][j] + v[3][j]));
                         } else {
-                            y = ((v[0][j] + v[1][j]) + v[2][j]) + v[3][j];
+                            y = s0 * (((v[0][j] + v[1][j]) + v[2][j]) + v[3][j]);
                             if constexpr (GATHER) y = act_t<ACT>(y);
                         }
                         h[4 * half + j] = ROWS ? w * y : y;
@@ -383,6 +407,13 @@ hipError_t launch_cfg(const DecArgs& a, hipStream_t stream) {
     const long long nwg = (long long)a.max_groups * a.nblk;
     if (nwg > 0x7fffffffLL) return hipErrorInvalidValue;
     if (nwg <= 0) return hipSuccess;
+    if (a.w8) {
+        // fp8 codes are [N,K] for every GEMM (Nomic's fc2 runs the down mode)
+        constexpr int M8 = MODE == kFc2Rows ? kDownRows : MODE;
+        hipLaunchKernelGGL((moe_dec_gemv<DT, M8, RB, CPL, false, true>), dim3((int)nwg), dim3(64 * kDvWaves), 0,
+                           stream, a);
+        return hipGetLastError();
+    }
     // (Nomic's fc2 is [N,K] either way: no packed instance)
     if constexpr (MODE != kFc2Rows) {
         if (a.packed) {

@@ -175,6 +175,36 @@ def test_fused_moe_fp8_register_operand_kernel_accumulates_and_drops():
     assert_close(got, want, RTOL[O.BF16], "register-operand fp8 kernel, accumulate mode with dropped pairs")
 
 
+# The decode kernels (tile policy 18: the pairs grouped inside the GEMM
+# kernels, 16 codes per lane load as two MFMA operands, column scales in the
+# epilogue) forced on the same cases.
+@pytest.mark.parametrize("name,T,H,I,E,k,act,mt,dt,zipf", GEMV_CASES, ids=[c[0] for c in GEMV_CASES])
+def test_fused_moe_fp8_decode_kernels(name, T, H, I, E, k, act, mt, dt, zipf):
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, zipf, seed=250 + T)
+    candle_moe.set_tile_policy(candle_moe.TILE_DEC_GEMV)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
+    assert_close(got, want, RTOL[dt], f"{name} fp8 decode kernels vs f64 oracle")
+
+
+def test_fused_moe_fp8_decode_kernels_accumulate_and_drop():
+    T, H, I, E, k = 24, 512, 256, 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=293)
+    ri = ri.copy()
+    ri[::3, 1] = E + 5
+    init = O.to_dtype(O.randn((T, H), seed=294, std=0.5), O.BF16)
+    candle_moe.set_tile_policy(candle_moe.TILE_DEC_GEMV)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init)
+    assert_close(got, want, RTOL[O.BF16], "fp8 decode kernels, accumulate mode with dropped pairs")
+
+
 @pytest.mark.parametrize("mt", [O.QWEN3, O.NOMIC])
 def test_fused_moe_fp8_accumulates(mt):
     T, H, I, E, k = (16, 4096, 1536, 8, 2) if mt == O.QWEN3 else (16, 768, 3072, 8, 2)
