@@ -146,6 +146,7 @@ struct Problem {
     int split_target; // K splits: the kernels aim at this many workgroups (live tiles * splits)
     bool narrow1;     // fc1 GEMM on 128-column tiles of the 32-row kernel
     bool narrow2;     // pair-path down / fc2 GEMM on 128-column tiles of the 32-row kernel
+    int dec_ks1, dec_ks2;  // decode kernels: most K slices of the gate/up (fc1) and down (fc2) GEMMs
 };
 
 // CUs per XCD of the current device (its CUs over the 8 XCDs of MI355X), 0
@@ -166,11 +167,16 @@ static int cus_per_xcd() {
     return cached[dev];
 }
 
+// Every workspace starts with a fixed header, the same for every shape, whose
+// counters the library-owned workspaces hold at zero between calls: the
+// one-launch grouping's (offset 0, 256 bytes). The router's split partials
+// go after it.
+constexpr size_t kWsHeaderBytes = 256;
 struct Layout {
     size_t sync;  // 4 ints of the one-launch grouping (offset 0, 256 bytes)
     size_t offsets, block_counts, sorted_pair, tile_row, tile_exp, num_tiles;
     size_t k_offsets, k_block_counts, tok_sorted, tile_row2, tile_key2, num_tiles2, pair_dest;
-    size_t inter, acc, partial, counters, total;
+    size_t inter, acc, partial, counters, dec_meta, total;
 };
 
 // 0: choose per call; 1: always the pair path (pair rows or f32 atomics,
@@ -216,7 +222,7 @@ static Layout make_layout(const Problem& p) {
     const long long nb = grouping_blocks(p.P);
     const long long mt = grouping_max_tiles(p.P, p.E, p.BM);
     size_t o = 0;
-    L.sync = o; o += 256;
+    L.sync = o; o += kWsHeaderBytes;
     L.offsets = o; o += a256((size_t)(p.E + 2) * 4);
     L.block_counts = o; o += a256((size_t)(nb > 0 ? nb : 1) * p.E * 4);
     L.sorted_pair = o; o += a256((size_t)(p.P > 0 ? p.P : 1) * 4);
@@ -238,9 +244,19 @@ static Layout make_layout(const Problem& p) {
     }
     L.inter = o; o += a256((size_t)p.P * p.I * es);
     L.acc = o;  // pair path: f32 accumulator [T, H], or the pair rows [T*k, H] (dtype)
-    if (!p.set_path) o += p.rows_path ? a256((size_t)p.P * p.H * es) : a256((size_t)p.T * p.H * 4);
+    if (p.cfg == kDecGemv) {
+        // decode kernels: the f32 partials of both GEMMs (one after the other)
+        const size_t nc1 = (size_t)(p.moe_type == kQwen3 ? 2 : 1) * p.I;
+        const size_t n1 = p.dec_ks1 > 1 ? (size_t)p.dec_ks1 * p.P * nc1 : 0;  // (ks == 1: rows in the dtype)
+        const size_t n2 = (size_t)p.dec_ks2 * p.P * p.H;
+        o += a256(std::max(n1, n2) * 4);
+    } else if (!p.set_path) {
+        o += p.rows_path ? a256((size_t)p.P * p.H * es) : a256((size_t)p.T * p.H * 4);
+    }
     // split-K partials and arrival counters, shared by the two GEMMs (they run
     // one after the other; the counters are left zero)
+    L.dec_meta = o;
+    if (p.cfg == kDecGemv) o += 256;  // decode kernels: the slices each GEMM chose
     L.partial = L.counters = o;
     if (p.split1 > 1 || p.split2 > 1) {
         // partial slots: live tiles * splits, at most split_target with the
@@ -272,6 +288,27 @@ static bool dec_gemv_fits(const Problem& p) {
            p.P * p.I * 2 < lim && p.P * p.H * 2 < lim && (long long)(p.H + 1024) * p.I * 2 < lim &&
            (long long)(p.I + 1024) * p.H * 2 < lim;
 }
+
+// Most K slices of a decode GEMM over N columns and K (the kernels choose
+// the slices from the experts a batch touches, up to this): cold weights
+// stream at the rate of the access pattern and of the workgroups reading
+// them (a probe over the Qwen3 T=8 gate/up weights, 176 MB: 128-byte runs of
+// k-rows on 168 workgroups 4.0 TB/s, 256-byte runs on 500-1000 workgroups
+// 5.9 TB/s), so slices let 128-column blocks (256-byte runs) fill the
+// device. Bounds: at least kDecMinSteps steps of 32 k per wave (kp waves
+// share a slice of one tensor) and f32 partials of at most kDecPartBytes.
+// Used where the weight stream is at least kDecSliceBytes (check_problem).
+constexpr int kDecMinSteps = 1;
+constexpr double kDecPartBytes = 16.0 * 1024 * 1024;
+constexpr double kDecSliceBytes = 128.0 * 1024 * 1024;
+static int dec_slices(long long P, int N, int K, int kp, int nc_mult) {
+    long long ks = cdiv(K, 32) / (kp * kDecMinSteps);
+    ks = std::min<long long>(ks, kDecMaxSlices);
+    ks = std::min<long long>(ks, (long long)(kDecPartBytes / ((double)std::max<long long>(P, 1) * N * nc_mult * 4)));
+    return (int)std::max<long long>(ks, 1);
+}
+// Workgroups of one round of the decode kernels: two per CU.
+static int dec_cap() { return 2 * 8 * std::max(cus_per_xcd(), 32); }
 
 // aligned16: input and weights start on 16-byte boundaries (the MFMA and f32
 // tiled kernels read them with 16-byte loads; otherwise the scalar kernel
@@ -495,6 +532,23 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         if (!p.set_path) p.split2 = choose(mt * p.n_tiles2, I);
         p.split1 = choose(mt * p.n_tiles1, H);
     }
+    p.dec_ks1 = p.dec_ks2 = 1;
+    if (p.cfg == kDecGemv) {
+        // K slices for the gate/up (fc1) GEMM only where they paid: few
+        // column blocks of 128 and a large weight stream. Measured steps
+        // (router + forward, graph-replayed, cold bf16 weights), sliced
+        // against not: Qwen3 T=8 / 64 65.1 / 80.1 against 73.3 / 84.1 us;
+        // Qwen3-30B-A3B T=1 / 16 29.6 / 83.4 against 29.0 / 78.4 us, Nomic
+        // T=16 36.4 against 35.1 us (the finishing launch costs more than
+        // the faster stream saves); fp8 weights (half the bytes) slower
+        // sliced too. The down / fc2 GEMM, whose finishing launch sums the
+        // pairs anyway, ran 1-3 us faster unsliced on every shape.
+        const bool q3 = p.moe_type == kQwen3;
+        const long long groups = std::min<long long>(P, E);
+        const double wbytes = (double)groups * (q3 ? 2 : 1) * H * I * (fp8 ? 1 : 2);
+        if (groups * cdiv(I, 128) < 256 && wbytes >= kDecSliceBytes)
+            p.dec_ks1 = dec_slices(P, I, H, q3 ? 2 : 4, q3 ? 2 : 1);
+    }
     return CANDLE_MOE_OK;
 }
 
@@ -505,15 +559,19 @@ struct Fp8Weights {
     const float* down_scale;
 };
 
-// Decode path (kDecGemv): gate/up (fc1) into inter [P, I] by pair, down
-// (fc2) into the pair rows [P, H], then each token's k rows summed in slot
-// order; the GEMM kernels group the pairs themselves (no grouping launch).
-// Columns per lane: the widest block that still gives every CU a workgroup.
-// [K,N] weights (trans): 8 or 4 columns (16 or 8-byte loads; 4-byte loads
-// ran the Qwen3 T=8 gate/up at 78 against 46 us); [N,K] weights (Nomic fc2,
-// 16-byte loads whatever the block): 8, 4 or 2 (T=16 fc2 22.3 -> 15.4 us
-// with 2).
-static int dec_cpl(long long groups, int N, bool trans) {
+// Decode path (kDecGemv): the gate/up (fc1) GEMM into inter [P, I] by pair
+// (with K slices: f32 partials, then a finishing launch that sums them and
+// applies the activation), the down (fc2) GEMM into f32 partials [ks][P][H],
+// then a finishing launch that sums each token's pairs (slices in order,
+// slots in order, one rounding). The GEMM kernels group the pairs themselves
+// (no grouping launch) and choose the slices from the touched experts.
+// Columns per lane: 8 with K slices (256-byte runs of [K,N] rows); without,
+// the widest block that still gives every CU a workgroup. [K,N] weights
+// (trans): 8 or 4 columns (16 or 8-byte loads; 4-byte loads ran the Qwen3
+// T=8 gate/up at 78 against 46 us); [N,K] weights (16-byte loads whatever
+// the block): 8, 4 or 2.
+static int dec_cpl(long long groups, int N, bool trans, int ks_lim) {
+    if (ks_lim > 1) return 8;
     const int narrowest = trans ? 4 : 2;
     for (int c = 8; c > narrowest; c /= 2)
         if (groups * cdiv(N, 16 * c) >= 256) return c;
@@ -524,14 +582,16 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
                        hipStream_t s, const Fp8Weights* f8) {
     const bool qwen3 = p.moe_type == kQwen3;
     void* inter = ws + L.inter;
-    void* rows = ws + L.acc;
+    float* part = reinterpret_cast<float*>(ws + L.acc);
+    int* meta = reinterpret_cast<int*>(ws + L.dec_meta);
     DecArgs d = {};
     d.A = x;
     d.B0 = gate;
     d.B1 = up;
     d.C = inter;
+    d.part = part;
+    d.meta = meta;
     d.idx = idx;
-    d.routing_w = rw;
     d.P = (int)p.P;
     d.E = p.E;
     d.K = p.H;
@@ -549,28 +609,46 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d.a_bytes = (long long)p.T * p.H * 2;
     d.max_groups = (int)std::min<long long>(p.P, p.E);
     d.rows_max = (int)std::min<long long>(p.P, p.T);
-    d.cpl = dec_cpl(d.max_groups, p.I, !p.packed && !f8);
+    d.cap = dec_cap();
+    d.ks_lim = p.dec_ks1;
+    d.cpl = dec_cpl(d.max_groups, p.I, !p.packed && !f8, d.ks_lim);
     d.nblk = cdiv(p.I, 16 * d.cpl);
+    const int mode1 = qwen3 ? kGateUp : kFc1;
     hipError_t e;
     {
         ProfScope ps(kSlotGemm1, s);
-        e = launch_dec_gemv(qwen3 ? kGateUp : kFc1, p.dtype, d, s);
+        e = launch_dec_gemv(mode1, p.dtype, d, s);
+        if (e == hipSuccess && d.ks_lim > 1) {
+            DecFinish f = {};
+            f.part = part;
+            f.meta = meta;
+            f.ks_lim = d.ks_lim;
+            f.P = (int)p.P;
+            f.N = p.I;
+            f.E = p.E;
+            f.T = p.T;
+            f.k_top = p.k;
+            f.act = p.act;
+            f.idx = idx;
+            f.scale0 = f8 ? f8->gate_scale : nullptr;
+            f.scale1 = f8 ? f8->up_scale : nullptr;
+            f.out = inter;
+            e = launch_dec_finish(mode1, p.dtype, f, s);
+        }
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe decode gate/up GEMM");
     DecArgs d2 = d;
     d2.A = inter;
     d2.B0 = qwen3 ? down : up;
     d2.B1 = nullptr;
-    d2.C = rows;
+    d2.C = nullptr;
     d2.K = p.I;
     d2.N = p.H;
     d2.ldb = (qwen3 && !p.packed && !f8) ? p.H : p.I;  // down [E][I][H] (packed / fp8 [E][H][I]); fc2 [E][H][I]
-    if (f8) {
-        d2.scale0 = qwen3 ? f8->down_scale : f8->up_scale;
-        d2.scale1 = nullptr;
-    }
+    d2.scale0 = d2.scale1 = nullptr;                   // (applied by the finishing launch)
     d2.a_bytes = p.P * p.I * 2;
-    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed && !f8);
+    d2.ks_lim = p.dec_ks2;
+    d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed && !f8, d2.ks_lim);
     d2.nblk = cdiv(p.H, 16 * d2.cpl);
     {
         ProfScope ps(kSlotGemm2, s);
@@ -579,7 +657,21 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     if (e != hipSuccess) return hip_fail(e, "fused_moe decode down GEMM");
     {
         ProfScope ps(kSlotFinal, s);
-        e = launch_pair_rows_sum(out, p.dtype, rows, idx, p.E, p.T, p.k, p.H, overwrite, s);
+        DecFinish f = {};
+        f.part = part;
+        f.meta = meta;
+        f.ks_lim = d2.ks_lim;
+        f.P = (int)p.P;
+        f.N = p.H;
+        f.E = p.E;
+        f.T = p.T;
+        f.k_top = p.k;
+        f.idx = idx;
+        f.routing_w = rw;
+        f.scale0 = f8 ? (qwen3 ? f8->down_scale : f8->up_scale) : nullptr;
+        f.out = out;
+        f.overwrite = overwrite ? 1 : 0;
+        e = launch_dec_finish(qwen3 ? kDownRows : kFc2Rows, p.dtype, f, s);
     }
     if (e != hipSuccess) return hip_fail(e, "fused_moe decode row sums");
     return CANDLE_MOE_OK;
@@ -821,9 +913,9 @@ static OwnedWs* owned_ws_locked(int dev, hipStream_t s, size_t need, hipError_t&
     void* mem = nullptr;
     err = hipMallocAsync(&mem, want, s);
     if (err != hipSuccess) return nullptr;
-    // the one-launch grouping's counters start at zero (a kernel, not a
-    // memset node, should the call be captured into a graph)
-    err = launch_fill_zero_f32(reinterpret_cast<float*>(mem), 64, s);
+    // the header's counters start at zero (a kernel, not a memset node,
+    // should the call be captured into a graph)
+    err = launch_fill_zero_f32(reinterpret_cast<float*>(mem), (long long)(kWsHeaderBytes / 4), s);
     if (err != hipSuccess) {
         (void)hipFreeAsync(mem, s);
         return nullptr;
@@ -1157,7 +1249,9 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
     // small batches split K over workgroups, with f32 partials in the
     // library-owned workspace of this (device, stream) (held while enqueuing,
     // as fused_moe does)
-    const size_t need = cm::router_ws_bytes(T, H, E, (int)dtype);
+    // (after the workspace header, whose counters stay zero)
+    const size_t rneed = cm::router_ws_bytes(T, H, E, (int)dtype);
+    const size_t need = rneed > 0 ? cm::kWsHeaderBytes + rneed : 0;
     hipError_t e = hipSuccess;
     if (need > 0) {
         int dev = 0;
@@ -1171,7 +1265,8 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
         e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
                                    reinterpret_cast<uint32_t*>(topk_indices),
                                    reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k, s,
-                                   reinterpret_cast<float*>(w->ptr), w->bytes);
+                                   reinterpret_cast<float*>(static_cast<char*>(w->ptr) + cm::kWsHeaderBytes),
+                                   w->bytes - cm::kWsHeaderBytes);
     } else {
         e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
                                    reinterpret_cast<uint32_t*>(topk_indices),

@@ -232,35 +232,63 @@ hipError_t launch_moe_gemm_w8(int mode, int dtype, int cfg, const GemmArgs& a, h
 hipError_t launch_w8_gemv(int mode, int dtype, const GemmArgs& a, hipStream_t stream);
 hipError_t launch_moe_gemm_f32(int mode, int cfg, const GemmArgs& a, hipStream_t stream);
 
-// Decode GEMMs over 16-bit weights in the API layout (moe_gemv_dec.hip).
-// Every workgroup groups the P pairs itself (P <= kDecMaxPairs, E <=
-// kDecMaxE) and takes the u-th touched expert, u = blockIdx / nblk, and
-// column block blockIdx % nblk of 16 * cpl output columns; its waves split
-// K. Modes: kGateUp, kFc1 (inter [P, N] by pair), kDownRows, kFc2Rows (rows
-// [P, N] = dtype(w_p * ...), summed per token by launch_pair_rows_sum).
+// Decode GEMMs (moe_gemv_dec.hip) over 16-bit weights (API layout or
+// pre-packed) or fp8 codes. Every workgroup groups the P pairs itself (P <=
+// kDecMaxPairs, E <= kDecMaxE), counts the touched experts U and splits K
+// into ks = min(cap / (U * nblk), ks_lim) slices (at least 1), so that the U
+// * nblk * ks items (expert, column block of 16 * cpl columns, slice) fill
+// one round of cap workgroups; the grid is max(cap, max_groups * nblk) and
+// workgroup w takes item w. ks goes to meta[0] (gate/up, fc1) or meta[1]
+// (down, fc2) for the finishing launch. Modes: kGateUp, kFc1 (ks == 1: inter
+// [P, N] by pair in the dtype; ks > 1: f32 partials), kDownRows, kFc2Rows
+// (always f32 partials of the unweighted sums). Partials: part[(s * P + p) *
+// NC + c], NC = 2N for kGateUp (gate at c, up at N + c), else N.
 constexpr int kDecMaxPairs = 1024;
 constexpr int kDecMaxE = 4096;
+constexpr int kDecMaxSlices = 16;
 struct DecArgs {
     const void* A;            // x [T, K] (kGateUp / kFc1) or inter [P, K] (kDownRows / kFc2Rows)
     const void* B0;           // gate / fc1 / down / fc2 weights, expert-major
     const void* B1;           // up weights (kGateUp)
-    void* C;                  // inter or rows [P, N] (dtype)
+    void* C;                  // inter [P, N] (dtype; kGateUp / kFc1 when ks == 1)
+    float* part;              // f32 partials, ks_lim * P * NC floats
+    int* meta;                // [2] slices of the last gate/up and down launches
     const uint32_t* idx;      // [P] expert of pair p (>= E: dropped)
-    const float* routing_w;   // [P]
     int P, E, K, N, k_top, act;
     long long strideB;        // elements per expert matrix
     int ldb;                  // row pitch of B: N for [K,N] weights, K for [N,K] (kFc2Rows)
     long long a_bytes;        // bytes of A (< 2^31)
     int nblk;                 // column blocks of 16 * cpl columns
-    int max_groups;           // touched experts at most (grid = max_groups * nblk)
+    int cap;                  // workgroups of one round (the items' target)
+    int ks_lim;               // most K slices (1 .. kDecMaxSlices)
+    int max_groups;           // touched experts at most
     int rows_max;             // > 16: row chunks of 32 (two MFMA row blocks), else 16
     int cpl;                  // columns per lane: 2, 4 or 8
     int packed;               // every B [N,K] (pre-packed weights, ldb = K)
     int w8;                   // fp8 e4m3 codes [E][N][K] (ldb = K) with f32 scales [E][N]
-    const float* scale0;      // (w8) gate / fc1 / down / fc2 column scales
+    const float* scale0;      // (w8) gate / fc1 column scales (kGateUp / kFc1 with ks == 1)
     const float* scale1;      // (w8) up column scales
 };
 hipError_t launch_dec_gemv(int mode, int dtype, const DecArgs& a, hipStream_t stream);
+// Finishing the K slices of a decode GEMM (fixed slice order: deterministic),
+// ks = meta[0] (gate/up, fc1) or meta[1] (down, fc2), as the GEMM stored it.
+// kGateUp / kFc1 (nothing to do when ks == 1): inter[p] = dtype(act(s0 *
+// sum_s gate) (* s1 * sum_s up)) for the valid pairs. kDownRows / kFc2Rows:
+// out[t] = dtype(out[t] (accumulate) + sum_j w_{t,j} * s0 * sum_s
+// part[s][t*k + j]) over the valid pairs of token t in slot order. s0 / s1:
+// fp8 column scales of the pair's expert, or 1.
+struct DecFinish {
+    const float* part;
+    const int* meta;
+    int ks_lim, P, N, E, T, k_top, act;
+    const uint32_t* idx;
+    const float* routing_w;   // (down / fc2)
+    const float* scale0;      // (fp8) gate / fc1 / down / fc2 column scales, else null
+    const float* scale1;      // (fp8) up column scales, else null
+    void* out;                // inter [P, N] or out [T, N] (dtype)
+    int overwrite;            // (down / fc2) write out instead of adding to it
+};
+hipError_t launch_dec_finish(int mode, int dtype, const DecFinish& f, hipStream_t stream);
 
 
 // fp8 weight preparation (fp8.hip): quantize [E][K][N] (kn) or [E][N][K]

@@ -1,12 +1,14 @@
 """The decode kernels (tile policy 18, candle-moe_amd/csrc/moe_gemv_dec.hip)
-against the CPU oracle: each workgroup groups the pairs itself, loads the
-weights straight into registers (transposing 8 x CPL blocks of [K,N] weights
-into MFMA operands) and splits K over its waves; the down / fc2 GEMM stores
-pair rows that the k-row sum adds up. Cases: the BASELINE decode shapes by
-default selection, and forced onto shapes that exercise K and column tails,
-dropped and repeated experts, more rows per expert than one chunk, both
-activations layouts ([K,N] and Nomic's [N,K] fc2), f16 and accumulate mode.
-Tolerances as tests/test_gpu_moe.py."""
+against the CPU oracle: each workgroup groups the pairs itself, counts the
+touched experts and takes one (expert, column block, K slice) item, loads the
+weights straight into registers (transposing 8 x 8 blocks of [K,N] weights
+into MFMA operands) and splits its slice over its waves; finishing launches
+sum the slices' f32 partials in slice order (then the activation, or the k
+pairs of a token in slot order). Cases: the BASELINE
+decode shapes by default selection, and forced onto shapes that exercise K
+and column tails, dropped and repeated experts, more rows per expert than one
+chunk, both weight layouts ([K,N] and Nomic's [N,K] fc2), f16 and accumulate
+mode; owned and caller workspaces bit for bit. Tolerances as tests/test_gpu_moe.py."""
 import numpy as np
 import pytest
 
@@ -96,3 +98,40 @@ def test_decode_kernels_match_the_32_row_kernel():
     finally:
         candle_moe.set_tile_policy(candle_moe.TILE_AUTO)
     assert_close(a, b, RTOL[O.BF16], "decode kernels vs 32-row kernel")
+
+
+# T, H, I, E, k, dtype, moe_type, act: K slices on both GEMMs (few experts,
+# long K), k = 8 over 64 experts, Nomic's [N,K] fc2
+FINISH = [
+    (8, 1024, 512, 8, 2, O.BF16, O.QWEN3, O.SILU),
+    (2, 512, 256, 64, 8, O.BF16, O.QWEN3, O.SILU),
+    (16, 256, 512, 8, 2, O.F16, O.NOMIC, O.GELU),
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,k,dt,mt,act", FINISH)
+def test_owned_and_caller_workspaces_agree(T, H, I, E, k, dt, mt, act):
+    # the library-owned workspace against a caller workspace: the same slices
+    # summed in the same order, bit for bit, in accumulate mode
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, dt, 760 + T, mt)
+    init = O.round_to(O.randn((T, H), seed=761), dt).astype(np.float64)
+    a = forced(lambda: run_raw(x, G, U, D, rw, ri, E, k, act, mt, dt, out_init=init))
+    b = forced(lambda: run_raw(x, G, U, D, rw, ri, E, k, act, mt, dt, out_init=init, workspace=True))
+    assert np.array_equal(a, b)
+    want = O.fused_moe(x, G, U, D, rw, ri, E=E, k=k, act=act, moe_type=mt, dtype=dt, mode=O.MODE_EXACT) + init
+    assert_close(a, want, RTOL[dt], "accumulate")
+
+
+@pytest.mark.parametrize("workspace", [False, True])
+def test_every_pair_dropped(workspace):
+    # no expert touched: the forward writes zeros, the raw symbol leaves its
+    # output as it was
+    T, H, I, E, k = 4, 256, 128, 8, 2
+    x, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 770, O.QWEN3)
+    ri = np.full_like(ri, 99)
+    init = O.round_to(O.randn((T, H), seed=771), O.BF16).astype(np.float64)
+    got = forced(lambda: run_raw(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16, out_init=init,
+                                 workspace=workspace))
+    assert np.array_equal(got, init)
+    fwd = forced(lambda: run_moe(x, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16))
+    assert not fwd.any()

@@ -119,3 +119,30 @@ def test_router_topk_errors():
     assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 4, (1 << 22) + 8, 8, 2, O.BF16, s) != 0
     assert "4194304" in candle_moe.last_error()
     assert L.candle_moe_router_topk(p(x), p(w), p(out), p(idx), p(idx), 0, 64, 8, 2, O.BF16, s) == 0
+
+
+def test_router_partials_leave_the_workspace_counters_alone():
+    # the small-batch router writes f32 partials into the same per-stream
+    # workspace whose header holds the one-launch grouping's counters (zero
+    # between calls): a prefill call with that grouping and a decode call
+    # right after it must still match the oracle and their caller-workspace
+    # runs bit for bit
+    from test_gpu_moe import run_raw
+
+    x = O.to_dtype(quantized((16, 2048), 8.0, 3), O.BF16)
+    w = O.to_dtype(quantized((128, 2048), 64.0, 4), O.BF16)
+    for _ in range(3):
+        gw, gi, ge = run_fused(x, w, 8, O.BF16)
+    ww, wi, we = O.topk_softmax(O.router_logits(x, w, O.BF16), 8)
+    assert np.array_equal(gi, wi)
+    from helpers import RTOL, assert_close, moe_inputs
+    for n, (T, H, I, E, k) in enumerate([(3000, 256, 128, 8, 2), (8, 1024, 512, 8, 2)]):
+        xs, G, U, D, rw, ri = moe_inputs(T, H, I, E, k, O.BF16, 780 + n, O.QWEN3)
+        run_fused(x, w, 8, O.BF16)  # partials just before the call
+        a = run_raw(xs, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16)
+        b = run_raw(xs, G, U, D, rw, ri, E, k, O.SILU, O.QWEN3, O.BF16, workspace=True)
+        assert np.array_equal(a, b), f"case {n}: owned workspace differs from a caller workspace"
+        rows = np.arange(0, T, max(1, T // 40))
+        want = O.fused_moe(xs[rows], G, U, D, rw[rows], ri[rows], E=E, k=k, act=O.SILU, moe_type=O.QWEN3,
+                           dtype=O.BF16, mode=O.MODE_F32ACC)
+        assert_close(a[rows], want, RTOL[O.BF16], f"case {n}")
