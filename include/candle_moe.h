@@ -217,7 +217,10 @@ int candle_moe_fused_moe_path_ex(int num_tokens, int hidden_dim, int intermediat
  *   token_expert_indices u32 [T,k] = j*T + t.
  *   hidden [T,H], router_weight [E,H] (candle Linear layout), both `dtype`,
  *   16-byte aligned; H a multiple of 8 (4 for f32), at most 2^22; 1 <= E <= 128.
- * Reads hidden once (HBM-bound); the logits never reach memory. */
+ * Reads hidden once (HBM-bound); the logits never reach memory. Small 16-bit
+ * batches over more than 32 experts (at most 8 tiles of 32 tokens) split the
+ * weight stream over workgroups, with f32 partial logits in the library's
+ * per-stream workspace (the one fused_moe keeps; allocated on first use). */
 int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight,
                            void* topk_indices, void* token_expert_indices, int num_tokens,
                            int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);
