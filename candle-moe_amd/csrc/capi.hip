@@ -204,10 +204,17 @@ static int g_combine_policy = 0;
 static int g_tile_policy = 0;
 // Grouping launches above kGroupSmallMax items: 0 one launch where the
 // workspace's counters are known to start at zero (library-owned
-// workspaces, each used by one stream) and the launch fits the device,
-// else two; 1 always two; 2 one launch whose workgroups all take the recount
-// fallback (tests).
+// workspaces, each used by one stream), the launch fits the device and the
+// pair job has at most kGroupOneMaxBlocks blocks, else two; 1 always two; 2
+// one launch whose workgroups all take the recount fallback (tests).
+// Beyond that many blocks the one launch's agent-scope fences (a release per
+// workgroup, an acquire in each waiter) cost more than the second launch:
+// Qwen3 T=32768 (64 blocks per job) 18.6-20.0 us in one launch against 14.1
+// us in two, and the gate/up GEMM after it 1370 against 1383 us;
+// Qwen3-30B-A3B T=4096 (32 blocks) 13.8 against 13.7 us; Nomic T=4096 (8
+// blocks) 11.6 against 12.5 us.
 static int g_grouping_mode = 0;
+constexpr int kGroupOneMaxBlocks = 32;
 
 static long long set_tiles_max(const Problem& p) {
     return (p.T + p.BM - 1) / p.BM + (p.nkeys < p.T ? p.nkeys : p.T);
@@ -727,7 +734,8 @@ static int run_moe(const Problem& p, const void* x, const void* gate, const void
         GroupJob tj = {};
         if (p.set_path) tj = set_grouping_job(idx, p.T, p.k, p.E, p.nkeys, p.BM, tb, pair_dest);
         ProfScope ps(kSlotGroup, s);
-        const bool one = sync_zero && g_grouping_mode != 1;
+        const bool one = sync_zero && g_grouping_mode != 1 &&
+                         (g_grouping_mode == 2 || grouping_blocks(p.P) <= kGroupOneMaxBlocks);
         const int cus = cus_per_xcd() > 0 ? 8 * cus_per_xcd() : 0;
         e = launch_groupings(pj, p.set_path ? &tj : nullptr, s,
                              one ? reinterpret_cast<int32_t*>(ws + L.sync) : nullptr, cus,

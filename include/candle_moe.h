@@ -189,8 +189,9 @@ int candle_moe_set_tile_policy(int policy);
 /* Grouping of fused_moe above 2048 items (process-wide; no counterpart in the
  * reference, whose preprocessing is /root/reference/kernels/preprocessing.cuh:5-313):
  * 0 = one launch (per-block histograms, a bounded wait for every block's
- *     counts, stable scatter) on library-owned workspaces and the
- *     no-allocation scratch, two launches on caller workspaces (default),
+ *     counts, stable scatter) on library-owned workspaces up to 32 blocks of
+ *     1024 pairs; two launches beyond, on caller workspaces and on the
+ *     no-allocation scratch (default),
  * 1 = always two launches (histogram; scan + scatter),
  * 2 = one launch in which every workgroup recounts all items itself instead
  *     of waiting (the fallback of a wait that runs out; for tests).
