@@ -579,7 +579,6 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
         }
         __syncthreads();  // the parts are read before the next row chunk writes them
     }
-
 }
 
 // The finishing launch: one thread per 4 consecutive columns of a pair
