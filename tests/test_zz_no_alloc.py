@@ -33,8 +33,8 @@ def _call(fn, x, G, U, D, rw, ri, E, k, act, mt, dt, init):
 # (T, H, I, E, k, dtype, moe_type, act): batches of more than 2048 pairs (the
 # multi-workgroup grouping, whose launches must not depend on what an earlier
 # call left in the shared array), a prefill batch on the pair-row path, then
-# decode batches on the 32-row kernels with K splits (split-K counters and the
-# f32 accumulator live in the shared array), each smaller than the last
+# decode batches on the decode kernels (their f32 partials and slice counts
+# live in the shared array) and the f32 kernels, each smaller than the last
 SEQUENCE = [
     (1100, 512, 256, 128, 2, O.BF16, O.QWEN3, O.SILU),
     (1536, 256, 128, 64, 2, O.F16, O.NOMIC, O.GELU),
