@@ -573,16 +573,31 @@ struct Fp8Weights {
 // slots in order, one rounding). The GEMM kernels group the pairs themselves
 // (no grouping launch) and choose the slices from the touched experts.
 // Columns per lane: 8 with K slices (256-byte runs of [K,N] rows); without,
-// the widest block that still gives every CU a workgroup. [K,N] weights
-// (trans): 8 or 4 columns (16 or 8-byte loads; 4-byte loads ran the Qwen3
-// T=8 gate/up at 78 against 46 us); [N,K] weights (16-byte loads whatever
-// the block): 8, 4 or 2.
+// the block whose items (touched experts x column blocks, estimated from
+// min(P, E)) fall into the fewest per CU for their number: items / ceil(items
+// / CUs) largest (a CU with two items takes twice as long as one with one),
+// the wider block on ties. [K,N] weights (trans): 8 or 4 columns (16 or
+// 8-byte loads; 4-byte loads ran the Qwen3 T=8 gate/up at 78 against 46 us).
+// [N,K] weights (16-byte loads of 16 columns whatever the block): 8, 6, 4, 3
+// or 2 (blocks of 48 and 96 columns put Qwen3's 1536 and Nomic's 3072
+// columns of 8 experts into 256 items).
 static int dec_cpl(long long groups, int N, bool trans, int ks_lim) {
     if (ks_lim > 1) return 8;
-    const int narrowest = trans ? 4 : 2;
-    for (int c = 8; c > narrowest; c /= 2)
-        if (groups * cdiv(N, 16 * c) >= 256) return c;
-    return narrowest;
+    const double cus = 8.0 * std::max(cus_per_xcd(), 32);
+    static const int kTrans[] = {8, 4}, kNK[] = {8, 6, 4, 3, 2};
+    const int* cand = trans ? kTrans : kNK;
+    const int ncand = trans ? 2 : 5;
+    int best = cand[0];
+    double best_b = -1.0;
+    for (int i = 0; i < ncand; ++i) {
+        const double items = (double)groups * cdiv(N, 16 * cand[i]);
+        const double b = items / std::ceil(items / cus);
+        if (b > best_b + 1e-9) {
+            best_b = b;
+            best = cand[i];
+        }
+    }
+    return best;
 }
 static int run_moe_dec(const Problem& p, const void* x, const void* gate, const void* up, const void* down,
                        const float* rw, const uint32_t* idx, void* out, bool overwrite, char* ws, const Layout& L,

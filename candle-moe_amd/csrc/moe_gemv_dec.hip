@@ -58,10 +58,10 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f3
 
 constexpr int kDvWaves = 4;  // waves per workgroup
 constexpr int kDvStep = 32;  // K per step (one MFMA deep)
-// steps in flight per wave: 4, or 2 for 8 columns per lane, so that a wave
-// stays within 256 registers and two workgroups share a CU
+// steps in flight per wave: 4, or 2 for 6 or 8 columns per lane, so that a
+// wave stays within 256 registers and two workgroups share a CU
 template <int CPL>
-constexpr int dec_ring() { return CPL == 8 ? 2 : 4; }
+constexpr int dec_ring() { return CPL >= 6 ? 2 : 4; }
 
 // Operand j of a transposed 8 x CPL block: r[t] holds k-row t of CPL
 // consecutive columns (pairs of 16-bit values, low half first); the result
@@ -284,7 +284,9 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     constexpr int KP = DUAL ? kDvWaves / 2 : kDvWaves;  // K parts per tensor
     constexpr int NB = TRANS ? CPL : WGC / 16;   // MFMA column blocks per step (operands)
     constexpr int NLD = TRANS ? 8 : NB;          // weight loads per lane per step
-    static_assert(CPL == 2 || CPL == 4 || CPL == 8, "columns per lane");
+    // (3 and 6 only for [N,K] weights, whose operands are 16 independent
+    // columns: blocks of 48 or 96 columns)
+    static_assert(CPL == 2 || CPL == 4 || CPL == 8 || (!TRANS && (CPL == 3 || CPL == 6)), "columns per lane");
     static_assert(!TRANS || NB == CPL, "operands");
 
     __shared__ uint32_t s_bm[kDecMaxE / 32];
@@ -620,14 +622,19 @@ hipError_t launch_cfg(const DecArgs& a, hipStream_t stream) {
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((moe_dec_gemv<DT, MODE, RB, CPL, false, false>), grid, block, 0, stream, a);
-    return hipGetLastError();
+    if constexpr (MODE == kFc2Rows || (CPL != 3 && CPL != 6)) {
+        hipLaunchKernelGGL((moe_dec_gemv<DT, MODE, RB, CPL, false, false>), grid, block, 0, stream, a);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;  // [K,N] weights: 2, 4 or 8 columns per lane
 }
 
 template <int DT, int MODE>
 hipError_t launch_mode(const DecArgs& a, hipStream_t stream) {
     const bool rb2 = a.rows_max > 16;
     if (a.cpl == 2) return rb2 ? launch_cfg<DT, MODE, 2, 2>(a, stream) : launch_cfg<DT, MODE, 1, 2>(a, stream);
+    if (a.cpl == 3) return rb2 ? launch_cfg<DT, MODE, 2, 3>(a, stream) : launch_cfg<DT, MODE, 1, 3>(a, stream);
+    if (a.cpl == 6) return rb2 ? launch_cfg<DT, MODE, 2, 6>(a, stream) : launch_cfg<DT, MODE, 1, 6>(a, stream);
     if (a.cpl == 4) return rb2 ? launch_cfg<DT, MODE, 2, 4>(a, stream) : launch_cfg<DT, MODE, 1, 4>(a, stream);
     return rb2 ? launch_cfg<DT, MODE, 2, 8>(a, stream) : launch_cfg<DT, MODE, 1, 8>(a, stream);
 }
@@ -646,7 +653,7 @@ hipError_t launch_dt(int mode, const DecArgs& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_dec_gemv(int mode, int dtype, const DecArgs& a, hipStream_t stream) {
-    if (a.cpl != 2 && a.cpl != 4 && a.cpl != 8) return hipErrorInvalidValue;
+    if (a.cpl != 2 && a.cpl != 3 && a.cpl != 4 && a.cpl != 6 && a.cpl != 8) return hipErrorInvalidValue;
     if (a.P > kDecMaxPairs || a.E > kDecMaxE || a.ks_lim < 1 || a.ks_lim > kDecMaxSlices || a.cap < 1)
         return hipErrorInvalidValue;
     const bool rows = mode == kDownRows || mode == kFc2Rows;

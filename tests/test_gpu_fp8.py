@@ -145,6 +145,9 @@ def test_fused_moe_fp8_matches_oracle(name, T, H, I, E, k, act, mt, dt, zipf):
 GEMV_CASES = CASES + [
     ("qwen3_rows24_T48", 48, 1024, 512, 4, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
     ("qwen3_skew_T96", 96, 512, 256, 8, 2, O.SILU, O.QWEN3, O.BF16, 2.0),
+    # blocks of 48 and 96 columns on the decode kernels, with column tails
+    ("qwen3_cols48_T16", 16, 512, 1504, 8, 2, O.SILU, O.QWEN3, O.BF16, 0.0),
+    ("nomic_cols96_T16", 16, 256, 3024, 8, 2, O.GELU, O.NOMIC, O.BF16, 0.0),
 ]
 
 

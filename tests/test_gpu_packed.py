@@ -71,6 +71,8 @@ CASES = [
     (8, 4096, 1536, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 0, 0),       # decode kernels
     (1, 2048, 768, 128, 8, O.BF16, O.QWEN3, O.SILU, 1.1, 0, 0),
     (16, 768, 3072, 8, 2, O.F16, O.NOMIC, O.GELU, 0.0, 0, 0),
+    (16, 512, 1504, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 0, 0),       # 48-column blocks, column tail
+    (16, 256, 3024, 8, 2, O.BF16, O.NOMIC, O.GELU, 0.0, 0, 0),       # 96-column blocks, column tail
     (64, 1024, 512, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 12, 0),      # 32-row kernel
     (64, 768, 3072, 8, 2, O.BF16, O.NOMIC, O.GELU, 0.0, 12, 0),
     (512, 1024, 512, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 5, 0),      # 128x128
