@@ -7,7 +7,7 @@ sum the slices' f32 partials in slice order (then the activation, or the k
 pairs of a token in slot order). Cases: the BASELINE
 decode shapes by default selection, and forced onto shapes that exercise K
 and column tails, dropped and repeated experts, more rows per expert than one
-chunk, both weight layouts ([K,N] and Nomic's [N,K] fc2), f16 and accumulate
+chunk, the most pairs over the most experts, both weight layouts ([K,N] and Nomic's [N,K] fc2), f16 and accumulate
 mode; owned and caller workspaces bit for bit. Tolerances as tests/test_gpu_moe.py."""
 import numpy as np
 import pytest
@@ -51,6 +51,17 @@ FORCED = [
 @pytest.mark.parametrize("T,H,I,E,k,dt,mt,act", FORCED)
 def test_forced_decode_kernels(T, H, I, E, k, dt, mt, act):
     forced(lambda: check_case(T, H, I, E, k, dt, mt, act=act, seed=710 + T))
+
+
+def test_decode_kernel_limits():
+    # the most pairs (1024) over the most experts (4096): about 1000 touched
+    # experts, more (expert, column block) items than one round of workgroups;
+    # then 1024 pairs over 2 experts (32 row chunks per workgroup)
+    for (T, H, I, E, k, seed) in [(128, 128, 64, 4096, 8, 740), (1024, 64, 96, 2, 1, 741)]:
+        def case():
+            assert candle_moe.fused_moe_kernel(T, H, I, E, k, O.BF16, O.QWEN3) == candle_moe.TILE_DEC_GEMV
+            check_case(T, H, I, E, k, O.BF16, O.QWEN3, seed=seed)
+        forced(case)
 
 
 def test_rows_beyond_one_chunk():
