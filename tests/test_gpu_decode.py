@@ -7,8 +7,9 @@ sum the slices' f32 partials in slice order (then the activation, or the k
 pairs of a token in slot order). Cases: the BASELINE
 decode shapes by default selection, and forced onto shapes that exercise K
 and column tails, dropped and repeated experts, more rows per expert than one
-chunk, the most pairs over the most experts, both weight layouts ([K,N] and Nomic's [N,K] fc2), f16 and accumulate
-mode; owned and caller workspaces bit for bit. Tolerances as tests/test_gpu_moe.py."""
+chunk, the most pairs over the most experts, both weight layouts ([K,N] and
+Nomic's [N,K] fc2), f16 and accumulate mode; owned and caller workspaces bit
+for bit. Tolerances as tests/test_gpu_moe.py."""
 import numpy as np
 import pytest
 
