@@ -193,6 +193,21 @@ def test_fused_moe_fp8_decode_kernels(name, T, H, I, E, k, act, mt, dt, zipf):
     assert_close(got, want, RTOL[dt], f"{name} fp8 decode kernels vs f64 oracle")
 
 
+def test_fused_moe_fp8_decode_kernels_at_their_limits():
+    # 1024 pairs (the most) over 4096 experts (the most): ~1000 touched
+    # experts, more items than one round of workgroups
+    T, H, I, E, k = 128, 128, 64, 4096, 8
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=280)
+    candle_moe.set_tile_policy(candle_moe.TILE_DEC_GEMV)
+    try:
+        assert candle_moe.fused_moe_kernel(T, H, I, E, k, O.BF16, O.QWEN3) == candle_moe.TILE_DEC_GEMV
+        got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, O.SILU, O.QWEN3, O.BF16)
+    assert_close(got, want, RTOL[O.BF16], "fp8 decode kernels, 1024 pairs over 4096 experts")
+
+
 def test_fused_moe_fp8_decode_kernels_accumulate_and_drop():
     T, H, I, E, k = 24, 512, 256, 8, 2
     x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=293)

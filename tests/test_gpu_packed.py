@@ -81,6 +81,7 @@ CASES = [
     (4096, 512, 256, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 7, 2),      # 256x256, expert sets
     (4096, 256, 192, 8, 2, O.F16, O.NOMIC, O.GELU, 0.0, 7, 2),
     (3000, 320, 200, 8, 2, O.BF16, O.QWEN3, O.SILU, 0.0, 0, 0),      # ragged tails
+    (128, 128, 64, 4096, 8, O.BF16, O.QWEN3, O.SILU, 0.0, 18, 0),   # decode kernels: 1024 pairs, 4096 experts
 ]
 
 
