@@ -170,39 +170,52 @@ def check(code: int) -> None:
 
 
 # ------------------------------------------------------------ descriptors
-def _torch_dtype_code(t) -> int:
-    import torch
+_DTYPE_CODES = None
 
-    m = {
-        torch.float16: DT_F16,
-        torch.bfloat16: DT_BF16,
-        torch.float32: DT_F32,
-        torch.int64: DT_I64,
-        torch.float64: DT_F64,
-        torch.uint8: DT_U8,
-    }
-    if hasattr(torch, "uint32"):
-        m[torch.uint32] = DT_U32
-    # int32 index tensors are taken as u32 bit patterns (torch's uint32
-    # support is partial); values must be non-negative.
-    m[torch.int32] = DT_U32
-    if t.dtype not in m:
+
+def _dtype_codes() -> dict:
+    global _DTYPE_CODES
+    if _DTYPE_CODES is None:
+        import torch
+
+        m = {
+            torch.float16: DT_F16,
+            torch.bfloat16: DT_BF16,
+            torch.float32: DT_F32,
+            torch.int64: DT_I64,
+            torch.float64: DT_F64,
+            torch.uint8: DT_U8,
+        }
+        if hasattr(torch, "uint32"):
+            m[torch.uint32] = DT_U32
+        # int32 index tensors are taken as u32 bit patterns (torch's uint32
+        # support is partial); values must be non-negative.
+        m[torch.int32] = DT_U32
+        _DTYPE_CODES = m
+    return _DTYPE_CODES
+
+
+def _torch_dtype_code(t) -> int:
+    code = _dtype_codes().get(t.dtype)
+    if code is None:
         raise CandleMoeError(CANDLE_MOE_ERR_INVALID, f"dtype {t.dtype} is not supported")
-    return m[t.dtype]
+    return code
 
 
 def describe(t) -> CmTensor:
-    """cm_tensor_t for a torch tensor (GPU tensors carry their ordinal)."""
+    """cm_tensor_t for a torch tensor (GPU tensors carry their ordinal).
+    (Called for every tensor of every call: kept to a few attribute reads.)"""
+    rank = t.dim()
+    if rank > MAX_RANK:
+        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, f"rank {rank} exceeds {MAX_RANK}")
     d = CmTensor()
-    if t.dim() > MAX_RANK:
-        raise CandleMoeError(CANDLE_MOE_ERR_INVALID, f"rank {t.dim()} exceeds {MAX_RANK}")
-    d.data = t.data_ptr() if t.numel() else None
     d.dtype = _torch_dtype_code(t)
-    d.rank = t.dim()
-    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
-        d.dims[i] = s
-        d.strides[i] = st
-    d.device = t.device.index if t.is_cuda else -1
+    d.data = t.data_ptr() if t.numel() else None
+    d.rank = rank
+    if rank:
+        d.dims[:rank] = t.shape
+        d.strides[:rank] = t.stride()
+    d.device = t.get_device()  # -1 for CPU tensors
     return d
 
 
