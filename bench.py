@@ -600,7 +600,9 @@ def bench_fp8_decode(torch, cm, dev, args):
     events around every launch, over 60 calls rotating across weight copies
     whose total exceeds the 256 MB last-level cache twice (cold weights),
     and the weight bytes each GEMM streams (touched experts x 2HI or HI x bytes
-    per weight) over its time."""
+    per weight) over its time. `gemm_speedup`: bf16 over fp8 time of the two
+    GEMMs; `launch_speedup`: the same over every launch of the forward
+    (grouping where the path has one, GEMMs, finishing launches)."""
     L = cm.lib()
     p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -670,6 +672,8 @@ def bench_fp8_decode(torch, cm, dev, args):
             entry[label] = us
         b, f = entry["bf16"], entry["fp8"]
         entry["gemm_speedup"] = round((b["gemm_gate_up"] + b["gemm_down"]) / (f["gemm_gate_up"] + f["gemm_down"]), 3)
+        launches = lambda d: sum(v for k_, v in d.items() if k_ in names)  # noqa: E731
+        entry["launch_speedup"] = round(launches(b) / launches(f), 3)
         res[f"{wname}_T{T}"] = entry
         del bf, f8
     return res

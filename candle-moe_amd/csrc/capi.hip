@@ -198,7 +198,7 @@ constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
 // over ~30 experts) 51.6 against 40.2. (The host cannot tell how many
 // experts a batch touches, so the bound is on the pairs.)
 constexpr long long kW8GemvPairs = 16;
-constexpr long long kW8DecPairs = 32;
+constexpr long long kW8DecPairs = 128;
 static int g_combine_policy = 0;
 // 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
@@ -393,9 +393,11 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         // Up to kW8DecPairs pairs the decode kernels instead (the pairs
         // grouped inside the GEMM kernels, no grouping launch; GEMM time at
         // Qwen3 T=16 / Qwen3-30B-A3B T=1 / Nomic T=16 48.7 / 19.3 / 22.6
-        // against 53.3 / 21.8 / 27.6 us; at 128 pairs (Qwen3 T=64,
-        // Qwen3-30B-A3B T=16) 62 / 51 against 54 / 40 us: the column blocks
-        // are sized for the touched experts' upper bound, min(pairs, E)).
+        // against 53.3 / 21.8 / 27.6 us). At 128 pairs (Qwen3 T=64,
+        // Qwen3-30B-A3B T=16) their GEMMs take 48.5 / 43.2 us against 48.4 /
+        // 39.5 us on the 32-row kernel, whose grouping launch (7.4 us) makes
+        // its steps the longer ones: graph-replayed steps 53.2 / 56.2 us
+        // against 56.8 / 59.3 us.
         p.cfg = (P <= kW8GemvPairs) ? kW8Gemv : (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
         if (P <= kW8DecPairs && dec_gemv_fits(p)) p.cfg = kDecGemv;
         if (g_tile_policy == kW8Gemv || g_tile_policy == kLdsRows32 || g_tile_policy == kLds256w8 ||

@@ -14,9 +14,10 @@
 //    so the grid is one round of two per CU;
 //  * its 4 waves split the slice (gate/up: two waves per tensor, two K
 //    halves each; otherwise four K parts) over its column block; each lane
-//    loads its weight chunks straight into registers, a ring of 32-wide K
-//    steps in flight, and meets the other waves once, at the end, where the
-//    parts are summed through LDS in a fixed order;
+//    loads its weight chunks straight into registers, a ring of K steps in
+//    flight (32 k wide; 64 on Nomic's fc2, 128 on fp8 codes), and meets the
+//    other waves once, at the end, where the parts are summed through LDS in
+//    a fixed order;
 //  * v_mfma_f32_16x16x32: A = the expert's rows (x rows gathered by pair, or
 //    intermediate rows by pair; 16 per row block), B = weight columns.
 //    [K,N] weights (gate / up / fc1 / down): lane (g, i) (g = lane / 16,
@@ -25,8 +26,11 @@
 //    values with v_perm into CPL MFMA operands: operand j holds the 8 k of
 //    column c_i + j, so MFMA j computes columns {c_i + j}. [N,K] weights
 //    (Nomic fc2, pre-packed, fp8): one 16-byte load is the operand of column
-//    n, k0 + 8g .. +7 (fp8: k0 + 16g .. +15, two operands). The A operand of
-//    lane (g, r) holds row r at the same k.
+//    n, 8 k (fp8: 16 k, two operands); a lane loads one such chunk per
+//    column and step (pre-packed gate/up, fc1, down: k0 + 8g .. +7, the k of
+//    the API layout's MFMAs) or two adjacent ones (fc2, fp8: 128 contiguous
+//    bytes of the column per lane group step). The A operand of lane (g, r)
+//    holds row r at the same k.
 // Workgroup outputs go through LDS: each wave stores its f32 part of the
 // block, then every thread sums the parts of 8 consecutive columns of one
 // row and stores them:
@@ -59,9 +63,11 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f3
 constexpr int kDvWaves = 4;  // waves per workgroup
 constexpr int kDvStep = 32;  // K per step (one MFMA deep)
 // steps in flight per wave: 4, or 2 for 6 or 8 columns per lane, so that a
-// wave stays within 256 registers and two workgroups share a CU
-template <int CPL>
-constexpr int dec_ring() { return CPL >= 6 ? 2 : 4; }
+// wave stays within 256 registers and two workgroups share a CU; halved where
+// each column takes WCH = 2 chunks of 16 bytes per step (the same bytes in
+// flight)
+template <int CPL, int WCH = 1>
+constexpr int dec_ring() { return (CPL >= 6 ? 2 : 4) / WCH; }
 
 // Operand j of a transposed 8 x CPL block: r[t] holds k-row t of CPL
 // consecutive columns (pairs of 16-bit values, low half first); the result
@@ -271,19 +277,30 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     // on pre-packed weights (PK) and on fp8 codes (W8)
     constexpr bool TRANS = (MODE != kFc2Rows) && !PK && !W8;
     // W8: OCP fp8 e4m3 codes [E][N][K] (one byte per weight) with per-column
-    // f32 scales. A step is 64 k: a lane's 16-byte load holds k0 + 16g .. +15
-    // of its column, the operands of two MFMAs (converted exactly to DT),
-    // and the A operand holds the same k of its row in two 16-byte loads.
-    constexpr int KSTEP = W8 ? 64 : kDvStep;
-    constexpr int KG = W8 ? 16 : 8;   // k per lane group per step
-    constexpr int WB = W8 ? 1 : 2;    // bytes per weight
+    // f32 scales. A step is 128 k: a lane's two 16-byte loads hold
+    // k0 + 32g .. +31 of its column, the operands of four MFMAs (converted
+    // exactly to DT), and the A operand holds the same k of its row in four
+    // 16-byte loads.
+    // fp8 codes and Nomic's fc2 ([N,K] weights): each lane reads WCH = 2
+    // adjacent 16-byte chunks of its column per step, so that the 4 lane
+    // groups cover 128 contiguous bytes of every column instead of 64
+    // (Qwen3 T=16 fp8 gate/up 27.6 -> 25.7 us, down 18.0 -> 16.2 us; Nomic
+    // T=16 bf16 fc2 15.4 -> 13.9 us). The other pre-packed GEMMs keep one
+    // chunk: the same k per MFMA as on the API layout, hence the same sums
+    // bit for bit.
+    constexpr int WCH = (W8 || MODE == kFc2Rows) ? 2 : 1;
+    constexpr int KSTEP = (W8 ? 64 : kDvStep) * WCH;
+    constexpr int KG = (W8 ? 16 : 8) * WCH;  // k per lane group per step
+    constexpr int KC = W8 ? 16 : 8;         // k per 16-byte weight chunk
+    constexpr int WB = W8 ? 1 : 2;          // bytes per weight
+    constexpr int AH = (W8 ? 2 : 1) * WCH;   // 16-byte A loads per row and step
     constexpr bool ROWS = (MODE == kDownRows || MODE == kFc2Rows);
     constexpr int NT = 64 * kDvWaves;
     constexpr int WGC = 16 * CPL;                // output columns per workgroup
     constexpr int NPART = kDvWaves;              // f32 parts in LDS (gate/up: 2 gate, 2 up)
     constexpr int KP = DUAL ? kDvWaves / 2 : kDvWaves;  // K parts per tensor
     constexpr int NB = TRANS ? CPL : WGC / 16;   // MFMA column blocks per step (operands)
-    constexpr int NLD = TRANS ? 8 : NB;          // weight loads per lane per step
+    constexpr int NLD = TRANS ? 8 : NB * WCH;     // weight loads per lane per step
     // (3 and 6 only for [N,K] weights, whose operands are 16 independent
     // columns: blocks of 48 or 96 columns)
     static_assert(CPL == 2 || CPL == 4 || CPL == 8 || (!TRANS && (CPL == 3 || CPL == 6)), "columns per lane");
@@ -325,7 +342,7 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     // whole number of ring rounds (the steps past s_hi load zeros), so that
     // the ring loop needs no guard. The parts depend on K, the slices and the
     // waves only (not on the ring or the column block).
-    constexpr int RING = dec_ring<CPL>();
+    constexpr int RING = dec_ring<CPL, WCH>();
     const int nks = (K + KSTEP - 1) / KSTEP;
     const int nparts = KP * ks;
     const int per = (nks + nparts - 1) / nparts;
@@ -340,7 +357,7 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     for (int b = 0; b < NB; ++b) ncol[b] = TRANS ? col0 + CPL * li + b : col0 + 16 * b + li;
 
     // per-lane weight offsets, fixed: [K,N]: k-row 8g, columns ncol[0] ..;
-    // [N,K]: column ncol[b], k 8g. A lane whose columns lie past N starts at
+    // [N,K]: column ncol[b], k KG*g. A lane whose columns lie past N starts at
     // kOob. (Every offset stays below 2^32: kOob plus less than the expert's
     // 2^31 bytes.)
     const uint32_t ldb2 = (uint32_t)a.ldb * (uint32_t)WB;  // bytes per weight row
@@ -348,7 +365,7 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
 #pragma unroll
     for (int b = 0; b < (TRANS ? 1 : NB); ++b)
         wlane[b] = ncol[b] < N ? (TRANS ? 8u * (uint32_t)g * ldb2 + 2u * (uint32_t)ncol[0]
-                                        : (uint32_t)ncol[b] * ldb2 + 16u * (uint32_t)g)
+                                        : (uint32_t)ncol[b] * ldb2 + (uint32_t)(KG * WB) * (uint32_t)g)
                                : kOob;
 
     // ring of steps: weight chunks (CPL 16-bit values each for [K,N], 8 for
@@ -357,15 +374,23 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     // lane's k positions past K read zeros (kOob).
     constexpr int WDW = TRANS ? CPL / 2 : 4;  // dwords per weight load
     uint32_t wv[RING][NLD][WDW];
-    u32x4 xv[RING][RB][W8 ? 2 : 1];
+    u32x4 xv[RING][RB][AH];
+    // this lane's k of step s, chunk c, inside the wave's part and K (K is a
+    // multiple of KC: a chunk lies wholly inside or outside). Bitwise, not
+    // short-circuit: a branch on the uniform s < s_hi made the compiler wait
+    // for every load in flight at it.
+    auto k_ok = [&](int s, int c) {
+        return (s < s_hi) & (s * KSTEP + KG * g + KC * c < K);
+    };
     auto load_w = [&](int i, int st) {
         const int s = s_lo + st;
-        const bool kok = s < s_hi && s * KSTEP + KG * g < K;  // this lane's k of the step
 #pragma unroll
         for (int t = 0; t < NLD; ++t) {
+            const int c = TRANS ? 0 : t % WCH;
+            const bool kok = k_ok(s, c);
             uint32_t o;
             if constexpr (TRANS) o = kok ? wlane[0] + (uint32_t)(s * KSTEP + t) * ldb2 : kOob;
-            else o = kok ? wlane[t] + (uint32_t)(s * KSTEP * WB) : kOob;
+            else o = kok ? wlane[t / WCH] + (uint32_t)(s * KSTEP * WB + 16 * c) : kOob;
             if constexpr (WDW == 4) {
                 const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0);
 #pragma unroll
@@ -404,13 +429,15 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
             for (int b = 0; b < NB; ++b) acc[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
         auto load_a = [&](int i, int st) {
             const int s = s_lo + st;
-            const bool kok = s < s_hi && s * KSTEP + KG * g < K;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int h = 0; h < (W8 ? 2 : 1); ++h)
+                for (int h = 0; h < AH; ++h) {
+                    // load h holds the k of weight chunk h / (AH / WCH)
+                    const bool kok = k_ok(s, h / (AH / WCH));
                     xv[i][rb][h] = __builtin_amdgcn_raw_buffer_load_b128(
                         rx, kok ? abase[rb] + (uint32_t)(s * KSTEP) * 2u + 16u * h : kOob, 0, 0);
+                }
         };
         auto load = [&](int i, int st) {
             load_w(i, st);
@@ -420,26 +447,36 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 if constexpr (W8) {
-                    // codes k0 + 16g .. +7 and .. +15 of column b: two operands
-                    const u32x4 wl = fp8x8_to<DT>(u32x2{wv[i][b][0], wv[i][b][1]});  // exact in DT
-                    const u32x4 wh = fp8x8_to<DT>(u32x2{wv[i][b][2], wv[i][b][3]});
+                    // chunk c: codes k0 + KG g + 16c .. +7 and .. +15 of
+                    // column b, two operands; A loads 2c and 2c + 1 hold the
+                    // same k of the row
 #pragma unroll
-                    for (int rb = 0; rb < RB; ++rb) {
-                        acc[rb][b] = mfma16<DT>(xv[i][rb][0], wl, acc[rb][b]);
-                        acc[rb][b] = mfma16<DT>(xv[i][rb][1], wh, acc[rb][b]);
+                    for (int c = 0; c < WCH; ++c) {
+                        const uint32_t(&w)[WDW] = wv[i][b * WCH + c];
+                        const u32x4 wl = fp8x8_to<DT>(u32x2{w[0], w[1]});  // exact in DT
+                        const u32x4 wh = fp8x8_to<DT>(u32x2{w[2], w[3]});
+#pragma unroll
+                        for (int rb = 0; rb < RB; ++rb) {
+                            acc[rb][b] = mfma16<DT>(xv[i][rb][2 * c], wl, acc[rb][b]);
+                            acc[rb][b] = mfma16<DT>(xv[i][rb][2 * c + 1], wh, acc[rb][b]);
+                        }
+                    }
+                } else if constexpr (!TRANS) {
+                    // chunk c: k0 + KG g + 8c .. +7 of column b, A load c
+#pragma unroll
+                    for (int c = 0; c < WCH; ++c) {
+                        const uint32_t(&w)[WDW] = wv[i][b * WCH + c];
+                        const u32x4 bop = u32x4{w[0], w[1], w[2], w[3]};
+#pragma unroll
+                        for (int rb = 0; rb < RB; ++rb) acc[rb][b] = mfma16<DT>(xv[i][rb][c], bop, acc[rb][b]);
                     }
                 } else {
-                    u32x4 bop;
-                    if constexpr (TRANS) {
-                        uint32_t r[8][CPL / 2];
+                    uint32_t r[8][CPL / 2];
 #pragma unroll
-                        for (int t = 0; t < 8; ++t)
+                    for (int t = 0; t < 8; ++t)
 #pragma unroll
-                            for (int d = 0; d < CPL / 2; ++d) r[t][d] = wv[i][t][d];
-                        bop = column_operand<CPL>(r, b);
-                    } else {
-                        bop = u32x4{wv[i][b][0], wv[i][b][1], wv[i][b][2], wv[i][b][3]};
-                    }
+                        for (int d = 0; d < CPL / 2; ++d) r[t][d] = wv[i][t][d];
+                    const u32x4 bop = column_operand<CPL>(r, b);
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) acc[rb][b] = mfma16<DT>(xv[i][rb][0], bop, acc[rb][b]);
                 }

@@ -138,6 +138,23 @@ def test_fused_moe_fp8_matches_oracle(name, T, H, I, E, k, act, mt, dt, zipf):
     assert_close(got, want, RTOL[dt], f"{name} fp8 vs f64 oracle on the dequantized weights")
 
 
+# The 32-row LDS-DMA kernel (tile policy 12; by default from 129 pairs up to
+# 32 rows per touched expert) forced on decode cases.
+ROWS32_CASES = [c for c in CASES if c[0] in ("qwen3_T32", "qwen3_T64", "qwen3_30b_T16", "nomic_T16", "qwen3_odd_T5")]
+
+
+@pytest.mark.parametrize("name,T,H,I,E,k,act,mt,dt,zipf", ROWS32_CASES, ids=[c[0] for c in ROWS32_CASES])
+def test_fused_moe_fp8_32_row_kernel(name, T, H, I, E, k, act, mt, dt, zipf):
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, zipf, seed=350 + T)
+    candle_moe.set_tile_policy(candle_moe.TILE_ROWS32)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    finally:
+        candle_moe.set_tile_policy(0)
+    want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
+    assert_close(got, want, RTOL[dt], f"{name} 32-row fp8 kernel vs f64 oracle")
+
+
 # The register-operand decode kernel (tile policy 17; by default only up to
 # 16 pairs) forced on every decode case: K and N tails, tiles
 # of more than 16 rows (two row blocks) and more than 32 (several tiles per
@@ -178,9 +195,9 @@ def test_fused_moe_fp8_register_operand_kernel_accumulates_and_drops():
     assert_close(got, want, RTOL[O.BF16], "register-operand fp8 kernel, accumulate mode with dropped pairs")
 
 
-# The decode kernels (tile policy 18: the pairs grouped inside the GEMM
-# kernels, 16 codes per lane load as two MFMA operands, column scales in the
-# epilogue) forced on the same cases.
+# The decode kernels (tile policy 18, by default up to 128 pairs: the pairs
+# grouped inside the GEMM kernels, two 16-code loads per lane and column as
+# four MFMA operands, column scales in the epilogue) forced on the same cases.
 @pytest.mark.parametrize("name,T,H,I,E,k,act,mt,dt,zipf", GEMV_CASES, ids=[c[0] for c in GEMV_CASES])
 def test_fused_moe_fp8_decode_kernels(name, T, H, I, E, k, act, mt, dt, zipf):
     x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, zipf, seed=250 + T)
