@@ -301,9 +301,10 @@ int candle_moe_dequantize_fp8(const void* codes, const float* scales, int num_ex
  * up_q = fc2 codes [E][H][I] with up_scale [E][H]; down_q and down_scale
  * unused. Activations f16 or bf16;
  * hidden_dim and intermediate_dim multiples of 16; every tensor 16-byte
- * aligned. Runs the 32-row GEMM kernel for decode batches (at most 32 pairs
- * per touched expert) and the 8-wave 256x256 kernel beyond, with the combine
- * path chosen as for fused_moe (expert sets or pairs). */
+ * aligned. Runs the decode kernels up to 128 pairs (at most 1024 pairs and
+ * 4096 experts), the 32-row GEMM kernel beyond that up to 32 pairs per
+ * touched expert and the 8-wave 256x256 kernel past it, with the combine path
+ * chosen as for fused_moe (expert sets or pairs). */
 int candle_moe_fused_moe_fp8(const void* input, const void* gate_q, const void* up_q, const void* down_q,
                              const float* gate_scale, const float* up_scale, const float* down_scale,
                              const void* routing_weights, const void* expert_indices, void* output, int num_tokens,
