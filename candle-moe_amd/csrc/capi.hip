@@ -669,9 +669,13 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
     d2.K = p.I;
     d2.N = p.H;
     d2.ldb = (qwen3 && !p.packed && !f8) ? p.H : p.I;  // down [E][I][H] (packed / fp8 [E][H][I]); fc2 [E][H][I]
-    d2.scale0 = d2.scale1 = nullptr;                   // (applied by the finishing launch)
     d2.a_bytes = p.P * p.I * 2;
     d2.ks_lim = p.dec_ks2;
+    // fp8 column scales: multiplied in by the GEMM when it is not K-sliced
+    // (its partials are then whole sums), else by the finishing launch
+    const float* s2 = f8 ? (qwen3 ? f8->down_scale : f8->up_scale) : nullptr;
+    d2.scale0 = d2.ks_lim == 1 ? s2 : nullptr;
+    d2.scale1 = nullptr;
     d2.cpl = dec_cpl(d.max_groups, p.H, qwen3 && !p.packed && !f8, d2.ks_lim);
     d2.nblk = cdiv(p.H, 16 * d2.cpl);
     {
@@ -692,7 +696,7 @@ static int run_moe_dec(const Problem& p, const void* x, const void* gate, const 
         f.k_top = p.k;
         f.idx = idx;
         f.routing_w = rw;
-        f.scale0 = f8 ? (qwen3 ? f8->down_scale : f8->up_scale) : nullptr;
+        f.scale0 = d2.ks_lim == 1 ? nullptr : s2;
         f.out = out;
         f.overwrite = overwrite ? 1 : 0;
         e = launch_dec_finish(qwen3 ? kDownRows : kFc2Rows, p.dtype, f, s);

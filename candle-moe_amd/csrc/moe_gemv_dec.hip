@@ -314,6 +314,9 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     // different banks)
     constexpr int SPW = WGC + 4;
     __shared__ __attribute__((aligned(16))) float s_part[NPART][RB * 16][SPW];
+    // fp8 down / fc2, unsliced: the block's column scales for the partials
+    constexpr bool SCALED = W8 && ROWS;
+    __shared__ float s_sc[SCALED ? WGC : 1];
 
     dec_assign<NT, TRANS>(a, ROWS ? 1 : 0, s_bm, s_idx, s_misc);
     const int e = s_misc[0];
@@ -408,6 +411,12 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
     // gathered (it depends on the expert only)
 #pragma unroll
     for (int i = 0; i < RING; ++i) load_w(i, i);
+    // (read into a register now, stored to LDS after the K loop: a store
+    // here would wait for the weight loads issued before it)
+    float sc_reg = 0.0f;
+    if constexpr (SCALED) {
+        if (a.scale0 != nullptr && tid < WGC && col0 + tid < N) sc_reg = a.scale0[(long long)e * N + col0 + tid];
+    }
     const int cnt = dec_rows<NT>(a, e, s_idx, s_rows, s_misc);
 
 
@@ -535,6 +544,9 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
                     for (int b = 0; b < NB; ++b) row[TRANS ? CPL * li + b : 16 * b + li] = acc[rb][b][v];
                 }
             }
+        if constexpr (SCALED) {
+            if (tid < WGC) s_sc[tid] = sc_reg;
+        }
         __syncthreads();
 
         // every thread: 8 consecutive output columns of one row; the parts
@@ -570,6 +582,15 @@ __global__ __launch_bounds__(64 * kDvWaves, 2) void moe_dec_gemv(DecArgs a) {
                 for (int tn = 0; tn < NT2; ++tn) {
                     float y[8];
                     part_sums(m, c8, tn, y);
+                    // fp8 down / fc2 unsliced: the column scales here (the
+                    // finishing launch's product s * y, the same f32 value),
+                    // so that it reads no scales
+                    if constexpr (SCALED) {
+                        if (a.scale0 != nullptr) {
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) y[j] *= s_sc[c8 + j];
+                        }
+                    }
                     float* dst = a.part + ((long long)sl * a.P + p) * NC + (long long)tn * N + col;
                     if (col + 8 <= N) {
                         *reinterpret_cast<f32x4*>(dst) = f32x4{y[0], y[1], y[2], y[3]};
