@@ -316,6 +316,13 @@ static int dec_slices(long long P, int N, int K, int kp, int nc_mult) {
 }
 // Workgroups of one round of the decode kernels: two per CU.
 static int dec_cap() { return 2 * 8 * std::max(cus_per_xcd(), 32); }
+// Most pairs the decode kernels take by default (16-bit weights; up to 32
+// per touched expert). Beyond, their items outnumber one round of
+// workgroups and the 32-row kernel is faster: Qwen3-30B-A3B steps at T=32 /
+// 48 / 64 / 128 (256 / 384 / 512 / 1024 pairs) 108 / 140 / 156 / 213 us on
+// the decode kernels against 115 / 126 / 134 / 149 us; Qwen3 T=128 (256
+// pairs) 102 against 115 us.
+constexpr long long kDecDefaultPairs = 256;
 
 // aligned16: input and weights start on 16-byte boundaries (the MFMA and f32
 // tiled kernels read them with 16-byte loads; otherwise the scalar kernel
@@ -405,7 +412,7 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
             p.cfg = g_tile_policy;
     } else if (p.mfma && !policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
-        if (P <= 32 * touched) p.cfg = dec_gemv_fits(p) ? kDecGemv : kLdsRows32;
+        if (P <= 32 * touched) p.cfg = P <= kDecDefaultPairs && dec_gemv_fits(p) ? kDecGemv : kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
         else if (H <= 2048 && P < 1024 * touched && (long long)cdiv(H, 256) * est_tiles(128) >= 512)
             p.cfg = kLds128x256o2;

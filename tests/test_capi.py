@@ -196,6 +196,9 @@ def test_moe_status_symbol_rejects_without_launch():
     # rows per expert; (E+1)^k keys too many for the expert-set path
     (1, 2048, 768, 128, 8, 0, "pairs", 18, True),
     (16, 2048, 768, 128, 8, 0, "pairs", 18, True),
+    (32, 2048, 768, 128, 8, 0, "pairs", 18, True),   # 256 pairs: the decode kernels' last size
+    (64, 2048, 768, 128, 8, 0, "pairs", 12, False),  # 512 pairs: the 32-row kernel (f32 atomics)
+    (128, 2048, 768, 128, 8, 0, "pairs", 12, False),
     (1024, 2048, 768, 128, 8, 0, "pairs", 14, True),
     (4096, 2048, 768, 128, 8, 0, "pairs", 14, True),
     (16384, 2048, 768, 128, 8, 0, "pairs", 7, True),
@@ -204,6 +207,7 @@ def test_moe_status_symbol_rejects_without_launch():
     # Qwen3 (H 4096): expert sets once the pair rows reach 256 MiB (T >= 16384)
     (8, 4096, 1536, 8, 2, 0, "pairs", 18, True),
     (64, 4096, 1536, 8, 2, 0, "pairs", 18, True),
+    (128, 4096, 1536, 8, 2, 0, "pairs", 18, True),
     (512, 4096, 1536, 8, 2, 0, "pairs", 5, True),
     (4096, 4096, 1536, 8, 2, 0, "pairs", 7, True),
     (8192, 4096, 1536, 8, 2, 0, "pairs", 7, True),
