@@ -166,11 +166,12 @@ int candle_moe_set_combine_policy(int policy);
  * LDS-DMA MFMA kernels: 5 = 128x128, 7 = 256x256 (8 waves),
  * 12 = 32x256 (for <= 32 rows per expert on average where 18 does not apply),
  * 14 = 128x256 (BK 32, two workgroups per CU);
- * 18 = the decode kernels (f16 / bf16, at most 1024 pairs and 4096
+ * 18 = the decode kernels (f16 / bf16 / fp8, at most 1024 pairs and 4096
  *     experts): no grouping launch (each workgroup groups the pairs in LDS),
- *     weights loaded straight into registers and transposed there, K split
- *     across the waves of a workgroup only; default for <= 32 rows per
- *     expert on average. By default 5 is taken for
+ *     weights loaded straight into registers (transposed there for the API
+ *     layout), K split across the waves of a workgroup and, for large
+ *     gate/up streams, across workgroups; default for <= 32 rows per expert
+ *     on average and at most 256 pairs (fp8: 128). By default 5 is taken for
  * <= 128 rows per expert where the 256x256 tile would give few workgroups,
  * 14 for < 1024 rows per expert with hidden_dim <= 2048 when the down GEMM
  * has at least two 128x256 tiles per CU, else 7.
@@ -179,9 +180,9 @@ int candle_moe_set_combine_policy(int policy);
  * (the scalar 64x64 kernel 0 when hidden_dim or intermediate_dim is not a
  * multiple of 4 or an operand is not 16-byte aligned).
  * 17 concerns fp8 weights only (candle_moe_fused_moe_fp8; fused_moe
- * treats it as 0): the register-operand decode kernel, taken by default for
- * at most 16 pairs (num_tokens x num_selected_experts); for fp8 weights 12
- * and 7 force the 32-row and the 256x256 kernel, other codes leave the fp8
+ * treats it as 0): the register-operand decode kernel (no longer a default:
+ * 18 takes those sizes); for fp8 weights 18, 12 and 7 force the decode
+ * kernels, the 32-row and the 256x256 kernel, other codes leave the fp8
  * choice automatic.
  * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
 int candle_moe_set_tile_policy(int policy);
