@@ -180,8 +180,9 @@ int candle_moe_set_combine_policy(int policy);
  * (the scalar 64x64 kernel 0 when hidden_dim or intermediate_dim is not a
  * multiple of 4 or an operand is not 16-byte aligned).
  * 17 concerns fp8 weights only (candle_moe_fused_moe_fp8; fused_moe
- * treats it as 0): the register-operand decode kernel (no longer a default:
- * 18 takes those sizes); for fp8 weights 18, 12 and 7 force the decode
+ * treats it as 0): the register-operand decode kernel, the default for at
+ * most 16 pairs only where 18 does not apply (more than 4096 experts, or
+ * operands beyond its 32-bit offsets); for fp8 weights 18, 12 and 7 force the decode
  * kernels, the 32-row and the 256x256 kernel, other codes leave the fp8
  * choice automatic.
  * Other codes are rejected with CANDLE_MOE_ERR_INVALID. */
