@@ -413,6 +413,15 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
     } else if (p.mfma && !policy) {
         const long long wgs256 = est_tiles(256) * cdiv(I, gemm_tile_cols(p.moe_type == kQwen3 ? kGateUp : kFc1, kLds256w8));
         if (P <= 32 * touched) p.cfg = P <= kDecDefaultPairs && dec_gemv_fits(p) ? kDecGemv : kLdsRows32;
+        // up to 128 rows per touched expert, where the 128x128 tile would
+        // leave the down GEMM too few tiles for the CUs (a narrow hidden
+        // dimension: Nomic's 768) and its K is long enough to split (I >=
+        // 1024), the 32-row kernel with its K splits: Nomic T=192 / 256 / 512
+        // steps 64.0 / 66.7 / 88.5 us on the 128x128 tile against 49.8 /
+        // 55.9 / 75.1 us. (Its f32 atomics make these sizes' results vary in
+        // the last bits from call to call, as on the decode sizes it takes.)
+        else if (P <= 128 * touched && I >= 1024 && est_tiles(128) * cdiv(H, 128) < 8LL * std::max(cus_per_xcd(), 32))
+            p.cfg = kLdsRows32;
         else if (wgs256 < 256 && P <= 128 * touched) p.cfg = kLds128;
         else if (H <= 2048 && P < 1024 * touched && (long long)cdiv(H, 256) * est_tiles(128) >= 512)
             p.cfg = kLds128x256o2;

@@ -182,12 +182,14 @@ def test_moe_status_symbol_rejects_without_launch():
 
 @pytest.mark.parametrize("T, H, I, E, k, mt, path, kernel, rows", [
     # Nomic (H 768, moe_type 1): the down GEMM's 3 column tiles never fill the
-    # CUs twice on the two-per-CU tile; few rows per expert take the 128x128
-    # tile, the rest the 256x256 tile; its pair rows (T*k*H 16-bit values)
-    # stay below 256 MiB, so the pair path with pair rows throughout; decode
+    # CUs twice on the two-per-CU tile; up to 128 rows per expert the 32-row
+    # kernel (the 128x128 tile would give its down GEMM too few tiles), the
+    # rest the 256x256 tile; its pair rows (T*k*H 16-bit values) stay below
+    # 256 MiB, so the pair path with pair rows on the tiled kernels; decode
     # batches (<= 32 rows per expert) the decode kernels (18, pair rows)
     (16, 768, 3072, 8, 2, 1, "pairs", 18, True),
-    (512, 768, 3072, 8, 2, 1, "pairs", 5, True),
+    (192, 768, 3072, 8, 2, 1, "pairs", 12, False),
+    (512, 768, 3072, 8, 2, 1, "pairs", 12, False),
     (1024, 768, 3072, 8, 2, 1, "pairs", 7, True),
     (4096, 768, 3072, 8, 2, 1, "pairs", 7, True),
     (12288, 768, 3072, 8, 2, 1, "pairs", 7, True),
