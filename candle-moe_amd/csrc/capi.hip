@@ -199,6 +199,17 @@ constexpr double kRowsMaxBytes = 2.0 * 1024 * 1024 * 1024;
 // experts a batch touches, so the bound is on the pairs.)
 constexpr long long kW8GemvPairs = 16;
 constexpr long long kW8DecPairs = 128;
+// fp8 weights beyond 32 rows per touched expert: the 32-row kernel streams
+// each touched expert's weights once per 32-row chunk, the 8-wave 256x256
+// kernel once per 256 rows but with mostly empty tiles and few workgroups
+// until the experts hold a few hundred rows each. The 32-row kernel wins
+// while that stream stays within this many bytes (fp8 step us, 32-row
+// against 256x256): 302 MB: Qwen3 T=256 75.8 / 103.0, Nomic T=1024 65.7 /
+// 87.9; 151 MB and less: Nomic T=192 / 256 / 512 37.2 / 44.5 / 50.3 against
+// 64.1 / 65.3 / 75.8; 604 MB: Qwen3 T=512 125.6 / 128.1, Nomic T=2048 107.9
+// / 97.4; 1.2 GB: Qwen3 T=1024 212.9 / 146.3, Qwen3-30B-A3B T=1024 297.1 /
+// 250.8. (Measured up to 256 rows per touched expert; the rule stops there.)
+constexpr long long kW8Rows32StreamBytes = 384LL << 20;
 static int g_combine_policy = 0;
 // 0: choose the GEMM kernel per call; a shipped TileCfg code: force it.
 static int g_tile_policy = 0;
@@ -395,7 +406,9 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         // decode batches stream each touched expert's weights once per row
         // tile: up to kW8GemvPairs pairs the register-operand kernel (no LDS
         // staging, no K splits across workgroups), up to 32 rows per touched
-        // expert the 32-row tile kernel; beyond, the 8-wave 256x256 kernel.
+        // expert, or up to 256 while its weight stream stays within
+        // kW8Rows32StreamBytes, the 32-row tile kernel; beyond, the 8-wave
+        // 256x256 kernel.
         // Tile policies 17, 12 and 7 force one of them.
         // Up to kW8DecPairs pairs the decode kernels instead (the pairs
         // grouped inside the GEMM kernels, no grouping launch; GEMM time at
@@ -405,7 +418,10 @@ static int check_problem(int T, int H, int I, int E, int k, int act, uint32_t mo
         // 39.5 us on the 32-row kernel, whose grouping launch (7.4 us) makes
         // its steps the longer ones: graph-replayed steps 53.2 / 56.2 us
         // against 56.8 / 59.3 us.
-        p.cfg = (P <= kW8GemvPairs) ? kW8Gemv : (P <= 32 * touched) ? kLdsRows32 : kLds256w8;
+        const long long w8_bytes = (p.moe_type == kQwen3 ? 3LL : 2LL) * H * I;  // one expert's codes
+        const bool rows32 = P <= 32 * touched ||
+                            (P <= 256 * touched && est_tiles(32) * w8_bytes <= kW8Rows32StreamBytes);
+        p.cfg = (P <= kW8GemvPairs) ? kW8Gemv : rows32 ? kLdsRows32 : kLds256w8;
         if (P <= kW8DecPairs && dec_gemv_fits(p)) p.cfg = kDecGemv;
         if (g_tile_policy == kW8Gemv || g_tile_policy == kLdsRows32 || g_tile_policy == kLds256w8 ||
             (g_tile_policy == kDecGemv && dec_gemv_fits(p)))

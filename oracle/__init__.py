@@ -167,6 +167,8 @@ def fused_moe(x, gate, up, down, w, idx, *, E: int, k: int, act: int, moe_type: 
     w = np.ascontiguousarray(w, dtype=np.float32)
     idx = np.ascontiguousarray(idx, dtype=np.uint32)
     r = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
+    if r is not None and len(np.unique(r)) != len(r):
+        raise ValueError("fused_moe: rows must be distinct (the C oracle fills one output row per token)")
     nr = T if r is None else len(r)
     out = np.zeros((nr, H), np.float64)
     oi = None if out_init is None else np.ascontiguousarray(out_init, dtype=np.float64)

@@ -264,19 +264,25 @@ def test_fused_moe_fp8_drops_out_of_range_experts():
     assert_close(got, want, RTOL[O.BF16], "fp8 with dropped pairs")
 
 
+@pytest.mark.parametrize("policy", [0, candle_moe.TILE_W8])
 @pytest.mark.parametrize("mt,T,H,I,act,dt", [
     (O.QWEN3, 600, 256, 192, O.SILU, O.BF16),
     (O.NOMIC, 700, 320, 256, O.GELU, O.F16),
     (O.QWEN3, 333, 208, 272, O.RELU, O.F16),   # sizes off the 64-element tiles
 ])
-def test_fused_moe_fp8_prefill_kernel_all_rows(mt, T, H, I, act, dt):
-    # beyond 32 pairs per touched expert the fp8 path runs the 8-wave 256x256
-    # kernel (gate/up or fc1, then the pair-row down / fc2 and the row sums)
+def test_fused_moe_fp8_prefill_kernel_all_rows(mt, T, H, I, act, dt, policy):
+    # 40-90 pairs per touched expert over small weights: by default the 32-row
+    # kernel (its weight stream is small), forced the 8-wave 256x256 kernel
+    # (gate/up or fc1, then the pair-row down / fc2 and the row sums)
     E, k = 8, 2
     x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, dt, 0.0, seed=95 + T)
-    got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    candle_moe.set_tile_policy(policy)
+    try:
+        got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt)
+    finally:
+        candle_moe.set_tile_policy(0)
     want = _oracle(x, rw, ri, deq, E, k, act, mt, dt)
-    assert_close(got, want, RTOL[dt], "fp8 prefill kernel vs f64 oracle on the dequantized weights")
+    assert_close(got, want, RTOL[dt], f"fp8 (tile policy {policy}) vs f64 oracle on the dequantized weights")
 
 
 @pytest.mark.parametrize("mt,T,H,I,E,k,act,dt,zero_cols,accumulate", [
@@ -309,10 +315,14 @@ def test_fused_moe_fp8_expert_sets(mt, T, H, I, E, k, act, dt, zero_cols, accumu
         deq[name] = np.ascontiguousarray(np.transpose(d, (0, 2, 1))) if kn else d
     init = O.to_dtype(O.randn((T, H), seed=121, std=0.5), dt) if accumulate else None
     try:
+        # (expert sets run on the 8-wave kernel, which these sizes do not
+        # take by default)
+        candle_moe.set_tile_policy(candle_moe.TILE_W8)
         candle_moe.set_combine_policy(candle_moe.COMBINE_EXPERT_SETS)
         got = _run_fp8(x, rw, ri, dev, E, k, act, mt, dt, out_init=init)
     finally:
         candle_moe.set_combine_policy(candle_moe.COMBINE_AUTO)
+        candle_moe.set_tile_policy(0)
     want = _oracle(x, rw, ri, deq, E, k, act, mt, dt, out_init=init)
     assert_close(got, want, RTOL[dt], "fp8 expert sets vs f64 oracle on the dequantized weights")
     # and the pair path on the same inputs
@@ -324,12 +334,30 @@ def test_fused_moe_fp8_expert_sets(mt, T, H, I, E, k, act, dt, zero_cols, accumu
     assert_close(got2, want, RTOL[dt], "fp8 pair path vs f64 oracle")
 
 
+@pytest.mark.parametrize("mt,T,H,I,act,rows_every", [
+    (O.QWEN3, 256, 1024, 512, O.SILU, 1),     # 64 pairs per expert
+    (O.NOMIC, 1024, 768, 3072, O.GELU, 7),    # 256 pairs per expert, Nomic's size
+])
+def test_fused_moe_fp8_32_row_kernel_by_default_beyond_decode(mt, T, H, I, act, rows_every):
+    # beyond 32 pairs per touched expert with a small weight stream the
+    # default fp8 path stays on the 32-row kernel (its K splits, the grouping
+    # launch, f32 accumulation of the k pairs)
+    E, k = 8, 2
+    x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, mt, O.BF16, 0.0, seed=96 + T)
+    got = _run_fp8(x, rw, ri, dev, E, k, act, mt, O.BF16)
+    rows = sorted(set(range(0, T, rows_every)) | {T - 1})
+    xf = O.to_f32(x, O.BF16)
+    want = O.fused_moe(xf, deq["g"], deq["u"], deq.get("d"), rw, ri, E=E, k=k, act=act, moe_type=mt,
+                       dtype=O.F32, mode=O.MODE_EXACT, rows=rows)
+    assert_close(got[rows], want, RTOL[O.BF16], "fp8 default path beyond decode sizes (sampled rows)")
+
+
 def test_fused_moe_fp8_prefill_batch_sampled_rows():
     # 2048 tokens: the 8-wave 256x256 fp8 kernel with the tail's K splits
     T, H, I, E, k = 2048, 1024, 512, 8, 2
     x, rw, ri, dev, deq = _quantized_case(T, H, I, E, k, O.QWEN3, O.BF16, 0.0, seed=92)
     got = _run_fp8(x, rw, ri, dev, E, k, O.SILU, O.QWEN3, O.BF16)
-    rows = list(range(0, T, 29)) + [T - 1]
+    rows = sorted(set(range(0, T, 29)) | {T - 1})
     xf = O.to_f32(x, O.BF16)
     want = O.fused_moe(xf, deq["g"], deq["u"], deq["d"], rw, ri, E=E, k=k, act=O.SILU, moe_type=O.QWEN3,
                        dtype=O.F32, mode=O.MODE_EXACT, rows=rows)

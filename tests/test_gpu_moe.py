@@ -620,7 +620,7 @@ def check_accumulate(T, H, I, E, k, dt, mt, act, zipf, expect, combine, seed, ro
 @pytest.mark.parametrize("api", ["raw", "ws"])
 def test_accumulate_mode_prefill_paths(case, api):
     _, T, H, I, E, k, dt, mt, act, zipf, expect, combine = case
-    rows = list(range(0, T, max(1, T // 97))) + [T - 1]
+    rows = sorted(set(range(0, T, max(1, T // 97))) | {T - 1})
     check_accumulate(T, H, I, E, k, dt, mt, act, zipf, expect, combine, seed=90 + len(case[0]), rows=rows,
                      workspace=(api == "ws"))
 

@@ -226,6 +226,8 @@ def test_moe_linear_in_routing_weights_and_rows():
     rows = [0, 7, 29]
     c = O.fused_moe(x, G, U, D, rw, ri, rows=rows, **kw)
     assert np.array_equal(c, a[rows])
+    with pytest.raises(ValueError, match="distinct"):   # one output row per token
+        O.fused_moe(x, G, U, D, rw, ri, rows=[0, 7, 7], **kw)
     init = O.randn((T, H), seed=4).astype(np.float64)
     d = O.fused_moe(x, G, U, D, rw, ri, out_init=init, **kw)
     assert np.allclose(d, a + init, rtol=1e-12, atol=1e-12)
