@@ -164,7 +164,10 @@ int candle_moe_set_combine_policy(int policy);
  * 1 = register-staged MFMA kernel, 128x128 block tile (taken by default only
  *     when an operand exceeds the 2 GiB range of the LDS-DMA kernels);
  * LDS-DMA MFMA kernels: 5 = 128x128, 7 = 256x256 (8 waves),
- * 12 = 32x256 (for <= 32 rows per expert on average where 18 does not apply),
+ * 12 = 32x256 with K splits (for <= 32 rows per expert on average where 18
+ *     does not apply, and for <= 128 where intermediate_dim >= 1024 and the
+ *     128x128 tile would give the down GEMM fewer tiles than CUs, as with
+ *     Nomic's hidden_dim 768),
  * 14 = 128x256 (BK 32, two workgroups per CU);
  * 18 = the decode kernels (f16 / bf16 / fp8, at most 1024 pairs and 4096
  *     experts): no grouping launch (each workgroup groups the pairs in LDS),
@@ -305,8 +308,10 @@ int candle_moe_dequantize_fp8(const void* codes, const float* scales, int num_ex
  * hidden_dim and intermediate_dim multiples of 16; every tensor 16-byte
  * aligned. Runs the decode kernels up to 128 pairs (at most 1024 pairs and
  * 4096 experts), the 32-row GEMM kernel beyond that up to 32 pairs per
- * touched expert and the 8-wave 256x256 kernel past it, with the combine path
- * chosen as for fused_moe (expert sets or pairs). */
+ * touched expert, or up to 256 while it streams at most 384 MiB of weights
+ * (the touched experts' codes once per 32 rows), and the 8-wave 256x256
+ * kernel past it, with the combine path chosen as for fused_moe (expert
+ * sets, on the 256x256 kernel only, or pairs). */
 int candle_moe_fused_moe_fp8(const void* input, const void* gate_q, const void* up_q, const void* down_q,
                              const float* gate_scale, const float* up_scale, const float* down_scale,
                              const void* routing_weights, const void* expert_indices, void* output, int num_tokens,
