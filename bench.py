@@ -764,7 +764,7 @@ def graph_us(torch, calls, ncalls, reps, check):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):  # the stream whose library workspace is warm
         calls()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     for _ in range(2):

@@ -961,12 +961,21 @@ struct OwnedWs {
 static std::mutex g_ws_mu;
 static std::vector<OwnedWs> g_ws;
 
+// A stream being captured into a graph gets no new or larger workspace
+// (err = hipErrorStreamCaptureUnsupported): hipMallocAsync there would add an
+// allocation node to the caller's graph, memory the graph owns and releases
+// when it is destroyed, while this table would keep handing it out.
 static OwnedWs* owned_ws_locked(int dev, hipStream_t s, size_t need, hipError_t& err) {
     err = hipSuccess;
     OwnedWs* w = nullptr;
     for (auto& e : g_ws)
         if (e.device == dev && e.stream == s) w = &e;
     if (w && w->bytes >= need) return w;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        err = hipErrorStreamCaptureUnsupported;
+        return nullptr;
+    }
     // grow by at least 1.5x and to whole MiB, so that a slowly growing T
     // does not reallocate on every call
     size_t want = need + need / 2;
@@ -989,6 +998,15 @@ static OwnedWs* owned_ws_locked(int dev, hipStream_t s, size_t need, hipError_t&
     }
     g_ws.push_back(OwnedWs{dev, s, mem, want});
     return &g_ws.back();
+}
+
+static int ws_fail(const char* who, size_t need, hipError_t e) {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return set_error(CANDLE_MOE_ERR_WORKSPACE,
+                         "%s: the stream is being captured and its library workspace is missing or smaller than "
+                         "the %zu bytes this call needs: make one call of this size on the stream before capturing",
+                         who, need);
+    return set_error(CANDLE_MOE_ERR_WORKSPACE, "%s: hipMallocAsync(%zu) failed: %s", who, need, hipGetErrorString(e));
 }
 
 int trim_owned_workspaces() {
@@ -1036,8 +1054,7 @@ int fused_moe_impl(const void* x, const void* gate, const void* up, const void* 
     if (e != hipSuccess) return hip_fail(e, "fused_moe: hipGetDevice");
     std::lock_guard<std::mutex> lk(g_ws_mu);
     OwnedWs* w = owned_ws_locked(dev, s, L.total, e);
-    if (!w) return set_error(CANDLE_MOE_ERR_WORKSPACE, "fused_moe: hipMallocAsync(%zu) failed: %s", L.total,
-                             hipGetErrorString(e));
+    if (!w) return ws_fail("fused_moe", L.total, e);
     return run_moe(p, x, gate, up, down, reinterpret_cast<const float*>(rw), reinterpret_cast<const uint32_t*>(idx),
                    out, overwrite, reinterpret_cast<char*>(w->ptr), s, f8, true);
 }
@@ -1320,9 +1337,7 @@ int candle_moe_router_topk(const void* hidden, const void* router_weight, void* 
         if (e != hipSuccess) return cm::hip_fail(e, "router_topk: hipGetDevice");
         std::lock_guard<std::mutex> lk(cm::g_ws_mu);
         cm::OwnedWs* w = cm::owned_ws_locked(dev, s, need, e);
-        if (!w)
-            return cm::set_error(CANDLE_MOE_ERR_WORKSPACE, "router_topk: hipMallocAsync(%zu) failed: %s", need,
-                                 hipGetErrorString(e));
+        if (!w) return cm::ws_fail("router_topk", need, e);
         e = cm::launch_router_topk(hidden, router_weight, (int)dtype, reinterpret_cast<float*>(topk_weight),
                                    reinterpret_cast<uint32_t*>(topk_indices),
                                    reinterpret_cast<uint32_t*>(token_expert_indices), T, H, E, k, s,

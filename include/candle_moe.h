@@ -73,7 +73,11 @@ void topk_softmax(const void* gating_output, void* topk_weight, void* topk_indic
  * The workspace is library-owned: one buffer per (device, stream), allocated
  * stream-ordered (hipMallocAsync on `stream`) on first use, grown when a call
  * needs more and kept for the next call on that stream;
- * candle_moe_trim_workspaces releases them. No host synchronisation.
+ * candle_moe_trim_workspaces releases them. No host synchronisation. A stream
+ * being captured into a graph gets no new or larger workspace (the graph
+ * would own that memory): such a call fails with CANDLE_MOE_ERR_WORKSPACE
+ * before enqueuing anything, so make one call of the largest size on the
+ * stream before capturing it.
  */
 void fused_moe(const void* input, const void* gate_weights, const void* up_weights,
                const void* down_weights, const void* routing_weights, const void* expert_indices,
@@ -226,7 +230,8 @@ int candle_moe_fused_moe_path_ex(int num_tokens, int hidden_dim, int intermediat
  * Reads hidden once (HBM-bound); the logits never reach memory. Small 16-bit
  * batches over more than 32 experts (at most 8 tiles of 32 tokens) split the
  * weight stream over workgroups, with f32 partial logits in the library's
- * per-stream workspace (the one fused_moe keeps; allocated on first use). */
+ * per-stream workspace (the one fused_moe keeps; allocated on first use,
+ * never while the stream is being captured: see fused_moe). */
 int candle_moe_router_topk(const void* hidden, const void* router_weight, void* topk_weight,
                            void* topk_indices, void* token_expert_indices, int num_tokens,
                            int hidden_dim, int num_experts, int topk, uint32_t dtype, void* stream);

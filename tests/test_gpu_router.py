@@ -146,3 +146,64 @@ def test_router_partials_leave_the_workspace_counters_alone():
         want = O.fused_moe(xs[rows], G, U, D, rw[rows], ri[rows], E=E, k=k, act=O.SILU, moe_type=O.QWEN3,
                            dtype=O.BF16, mode=O.MODE_F32ACC)
         assert_close(a[rows], want, RTOL[O.BF16], f"case {n}")
+
+
+_REFUSED = []  # the graph of the refused capture, kept until the process ends
+
+
+def test_router_small_batches_replayed_from_cuda_graphs():
+    """The small-batch router (K split over workgroups, f32 partials in the
+    per-stream library workspace) in torch CUDA graphs captured on a stream
+    warmed by eager calls of the same sizes: every replay equals the eager
+    result bit for bit, with eager work between replays, also from a second
+    graph captured after the first one is destroyed (the workspace stays the
+    eager one). A call captured on a stream without a workspace is refused
+    before anything is enqueued."""
+    import torch
+
+    H, E, k, dt = 2048, 128, 8, O.BF16
+    w = O.to_dtype(quantized((E, H), 64.0, 11), dt)
+    xn = [O.to_dtype(quantized((T, H), 8.0, 20 + T), dt) for T in (1, 16, 128)]
+    wt = to_dev(w, dt)
+    xs = [to_dev(x, dt) for x in xn]
+    outs = [tuple(torch.full((x.shape[0], k), -1, dtype=d, device="cuda:0")
+                  for d in (torch.float32, torch.int32, torch.int32)) for x in xs]
+
+    def calls():
+        for x, (tw, ti, te) in zip(xs, outs):
+            candle_moe.router_topk(x, wt, tw, ti, te)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()
+    torch.cuda.synchronize()
+    ref = [tuple(t.clone() for t in o) for o in outs]
+    for x, (rw, ri, re) in zip(xn, ref):
+        ww, wi, we = O.topk_softmax(O.router_logits(x, w, dt), k)
+        assert np.array_equal(from_dev(ri).astype(np.uint32), wi)
+        assert np.array_equal(from_dev(re).astype(np.uint32), we)
+        np.testing.assert_allclose(from_dev(rw), ww, rtol=1e-6, atol=0)
+    for _ in range(2):  # the second graph is captured after the first is destroyed
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            calls()
+        for _ in range(3):
+            for o in outs:
+                for t in o:
+                    t.fill_(-1)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for o, r in zip(outs, ref):
+                assert all(torch.equal(a, b) for a, b in zip(o, r))
+        del graph
+    fresh = torch.cuda.Stream()
+    pad = torch.zeros(4, device="cuda:0")
+    refused = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(refused, stream=fresh):
+        pad.add_(1.0)
+        with pytest.raises(candle_moe.CandleMoeError, match="being captured") as err:
+            candle_moe.router_topk(xs[1], wt, *outs[1])
+        assert err.value.code == candle_moe.CANDLE_MOE_ERR_WORKSPACE
+    _REFUSED.append(refused)
