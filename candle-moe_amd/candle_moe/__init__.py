@@ -512,8 +512,9 @@ class FusedMoE:
 
 
 def trim_workspaces() -> None:
-    """Release the library-owned fused_moe workspaces (one per device and
-    stream, kept between calls); the next call allocates again."""
+    """Release the library-owned workspaces of fused_moe and router_topk (one
+    per device and stream, kept between calls; hipFree, which waits for the
+    device); the next call allocates again."""
     check(lib().candle_moe_trim_workspaces())
 
 

@@ -1014,15 +1014,18 @@ int trim_owned_workspaces() {
     int cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) cur = -1;
     hipError_t first = hipSuccess;
+    // hipFree, not hipFreeAsync on the stream of each workspace: that stream
+    // may have been destroyed since its last call (hipFree waits for the
+    // device instead)
     for (auto& e : g_ws) {
         if (!e.ptr) continue;
         if (e.device != cur) (void)hipSetDevice(e.device);
-        const hipError_t r = hipFreeAsync(e.ptr, e.stream);
+        const hipError_t r = hipFree(e.ptr);
         if (first == hipSuccess) first = r;
         if (e.device != cur && cur >= 0) (void)hipSetDevice(cur);
     }
     g_ws.clear();
-    return first == hipSuccess ? CANDLE_MOE_OK : hip_fail(first, "trim workspaces: hipFreeAsync");
+    return first == hipSuccess ? CANDLE_MOE_OK : hip_fail(first, "trim workspaces: hipFree");
 }
 
 int fused_moe_impl(const void* x, const void* gate, const void* up, const void* down, const void* rw,

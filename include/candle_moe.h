@@ -323,9 +323,10 @@ int candle_moe_fused_moe_fp8(const void* input, const void* gate_q, const void* 
                              int hidden_dim, int intermediate_dim, int num_experts, int num_selected_experts,
                              int activation_type, uint32_t moe_type, uint32_t dtype, void* stream);
 
-/* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status
- * and the FusedMoE forward (hipFreeAsync on the stream each was used on); the
- * next call allocates again. No counterpart in the reference, whose fused_moe
+/* Releases the library-owned workspaces of fused_moe / candle_moe_fused_moe_status,
+ * the FusedMoE forward and candle_moe_router_topk (hipFree: waits for the
+ * device, so the streams they were used on may already be destroyed; not
+ * while a stream is being captured); the next call allocates again. No counterpart in the reference, whose fused_moe
  * allocates and frees per call (/root/reference/kernels/moe.cu:570,770). */
 int candle_moe_trim_workspaces(void);
 
