@@ -342,7 +342,7 @@ __device__ __forceinline__ uint64_t group_key_max(uint64_t v) {
 // SIMD holds a single wave.
 // Selection (VPT <= 8): each lane sorts its VPT keys once; pass j takes the
 // group's largest head key and the lane that owned it drops its head.
-template <int VPT, int LPR, int OUTDT, int ESTR, int R>
+template <int VPT, int LPR, int OUTDT, int ESTR, int R, bool TIES = false>
 __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int e0, int g, int E, int k, int T,
                                                   const long long (&row)[R], const bool (&valid)[R],
                                                   void* __restrict__ wout, uint32_t* __restrict__ iout,
@@ -485,7 +485,19 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
                 for (int q = 0; q < VPT; ++q) s_row[e0 + q * ESTR] = x[0][q];
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                const float ee = exp_f32_f64(s_row[ej] - mf);
+                const float xj = s_row[ej];
+                if constexpr (TIES) {
+                    // equal logits (frequent among 16-bit logits) have equal
+                    // e, equal p and keys ordered by expert index, the exact
+                    // order: where every close pair is such a tie the keys
+                    // stand
+                    const float xprev = __int_as_float(__builtin_amdgcn_ds_bpermute(prev_addr, __float_as_int(xj)));
+                    if (__builtin_amdgcn_ballot_w64(near && !(xprev == xj)) == 0ull) {
+                        if (valid[0] && g < k) put(row[0], g, pj, ej);
+                        return;
+                    }
+                }
+                const float ee = exp_f32_f64(xj - mf);
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 if (g < c) {
@@ -665,7 +677,7 @@ __device__ __forceinline__ void softmax_topk_rows(const float (&x)[R][VPT], int 
     }
 }
 
-template <int VPT, int LPR, int OUTDT, int ESTR = 1>
+template <int VPT, int LPR, int OUTDT, int ESTR = 1, bool TIES = false>
 __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0, int g, int E, int k, int T,
                                                    long long row, bool valid, void* __restrict__ wout,
                                                    uint32_t* __restrict__ iout, uint32_t* __restrict__ eiout,
@@ -673,7 +685,7 @@ __device__ __forceinline__ void softmax_topk_group(const float (&x)[VPT], int e0
     const float(&xr)[1][VPT] = reinterpret_cast<const float(&)[1][VPT]>(x);
     const long long rr[1] = {row};
     const bool vr[1] = {valid};
-    softmax_topk_rows<VPT, LPR, OUTDT, ESTR, 1>(xr, e0, g, E, k, T, rr, vr, wout, iout, eiout, s_row);
+    softmax_topk_rows<VPT, LPR, OUTDT, ESTR, 1, TIES>(xr, e0, g, E, k, T, rr, vr, wout, iout, eiout, s_row);
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
@@ -699,8 +711,9 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restric
     // of the chosen experts back from it; written and read by one wave)
     constexpr bool FAST = VPT <= 8 && LPR * VPT <= 256 && LPR > 1;
     __shared__ float s_p[FAST ? 256 / LPR : 1][FAST ? LPR * VPT : 1];
-    softmax_topk_group<VPT, LPR, OUTDT>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
-                                        FAST ? s_p[threadIdx.x / LPR] : nullptr);
+    // (16-bit logits: the shortcut for exactly tied candidates)
+    softmax_topk_group<VPT, LPR, OUTDT, 1, INDT != kF32>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
+                                                         FAST ? s_p[threadIdx.x / LPR] : nullptr);
 }
 
 template <int VPT, int LPR, int INDT, int OUTDT>
@@ -767,8 +780,8 @@ __global__ __launch_bounds__(256) void topk_partials_kernel(const float* __restr
         x[j] = e0 + j < E ? Elem<DT>::to_f32(Elem<DT>::from_f32(x[j])) : -__builtin_inff();
     constexpr bool FAST = VPT <= 8 && LPR * VPT <= 256 && LPR > 1;
     __shared__ float s_p[FAST ? 256 / LPR : 1][FAST ? LPR * VPT : 1];
-    softmax_topk_group<VPT, LPR, kF32>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
-                                       FAST ? s_p[threadIdx.x / LPR] : nullptr);
+    softmax_topk_group<VPT, LPR, kF32, 1, true>(x, e0, g, E, k, T, row, valid, wout, iout, eiout,
+                                                FAST ? s_p[threadIdx.x / LPR] : nullptr);
 }
 
 // ------------------------------------------------------------------------
