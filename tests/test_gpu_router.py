@@ -198,6 +198,12 @@ def test_router_small_batches_replayed_from_cuda_graphs():
             for o, r in zip(outs, ref):
                 assert all(torch.equal(a, b) for a, b in zip(o, r))
         del graph
+    # the FusedMoE forward (fused_moe's workspace) is refused the same way
+    from helpers import moe_inputs
+
+    xm, G, U, D, rwm, rim = moe_inputs(8, 256, 128, 8, 2, dt, 5, O.QWEN3)
+    moe_args = [to_dev(a, dt) for a in (xm, G, U, D)] + [to_dev(rwm), to_dev(rim)]
+    moe = candle_moe.FusedMoE.new(8, 2, candle_moe.Activation.Silu)
     fresh = torch.cuda.Stream()
     pad = torch.zeros(4, device="cuda:0")
     refused = torch.cuda.CUDAGraph()
@@ -205,5 +211,8 @@ def test_router_small_batches_replayed_from_cuda_graphs():
         pad.add_(1.0)
         with pytest.raises(candle_moe.CandleMoeError, match="being captured") as err:
             candle_moe.router_topk(xs[1], wt, *outs[1])
+        assert err.value.code == candle_moe.CANDLE_MOE_ERR_WORKSPACE
+        with pytest.raises(candle_moe.CandleMoeError, match="being captured") as err:
+            moe.forward(*moe_args, O.QWEN3)
         assert err.value.code == candle_moe.CANDLE_MOE_ERR_WORKSPACE
     _REFUSED.append(refused)
